@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Paged-KV decode-step benchmark on one MI355X.
+
+One step = the device packs the step's metadata (slot_mapping, context
+lengths, -1 padded block tables, cu_seqlens_k) from the scheduler's
+per-sequence CSR state, builds the gather plan, then for each of the 28
+layers stores the 256 new K/V rows into the paged cache and gathers every
+sequence's K and V context into contiguous varlen buffers (one launch per
+layer).  Workload: Qwen3-VL-2B language-model KV shape (8 kv heads x 128,
+bf16), 256 live sequences with contexts log-uniform in [256, 16384] after
+16 evictions and 16 admissions, cache [2, 28, blocks, 256, 8, 128].
+
+Prints one JSON line:  value = store+gather algorithmic GB/s of the step
+(sum of the bytes the store and gather must move / step time), plus
+decode tokens/s, the HBM roofline of the dominant kernel (the varlen
+gather, timed live with events on its stream) and a CPU baseline (the
+oracle's C restatement on the host cores, bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+for _p in (REPO_ROOT, REPO_ROOT / "nano-vllm-multimodal_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "paged KV store+gather GB/s (fraction of HBM peak); decode-step tokens/s, 1 GPU"
+TRAFFIC_FILE = REPO_ROOT / "profiles" / "gather_varlen_decode_step_traffic.json"
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--layers", type=int, default=28)
+    p.add_argument("--check-layers", default="0", help="comma list of layers checked vs the oracle; '' = none")
+    p.add_argument("--cpu-baseline-layers", type=int, default=28,
+                   help="layers in the CPU baseline sample (0 disables it)")
+    p.add_argument("--cpu-baseline-repeats", type=int, default=2)
+    p.add_argument("--profile", action="store_true",
+                   help="run warmup + timed steps only (no check, no CPU baseline), for rocprofv3")
+    return p.parse_args(argv)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(the paged-KV store/gather path is rank-local; see DESIGN.md for sharding)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from nanokv import workloads
+    from nanokv.benchmark import MI355X_HBM_PEAK_GBPS, LaunchTimer, effective_bytes, summarize_latencies
+    from nanokv.packing import DevicePacker, SequenceBatch
+    from nanokv.paged_kv import create_paged_kv_backend
+
+    if torch.version.hip is None or not torch.cuda.is_available():
+        raise RuntimeError("bench.py needs a ROCm GPU")
+    device = torch.device("cuda", 0)
+    backend = create_paged_kv_backend("hip")
+
+    wl = workloads.build("decode_step", num_layers=args.layers)
+    L, B = wl.num_layers, wl.num_seqs
+    log(f"[bench] decode_step layers={L} seqs={B} blocks={wl.num_blocks} "
+        f"context_tokens={int(wl.num_tokens.sum())}")
+    cache = torch.empty((2, L, wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim),
+                        dtype=wl.dtype, device=device)
+    g = torch.Generator(device=device).manual_seed(workloads.seed_for("decode_step"))
+    for kv in range(2):
+        for layer in range(L):
+            cache[kv, layer].normal_(generator=g)
+    new_k = wl.key.to(device)
+    new_v = wl.value.to(device)
+    offsets, ids = wl.csr()
+    batch = SequenceBatch(wl.num_tokens, offsets, ids)
+    packer = DevicePacker(device, wl.block_size)
+    total = int(wl.num_tokens.astype(np.int64).sum())
+    k_out = torch.empty((total, wl.num_kv_heads, wl.head_dim), dtype=wl.dtype, device=device)
+    v_out = torch.empty_like(k_out)
+    stream = torch.cuda.current_stream(device)
+
+    def step(timer: LaunchTimer | None = None, store_timer: LaunchTimer | None = None):
+        ctx = packer.pack_decode(batch)
+        plan = backend.build_gather_plan(cache[0, 0], ctx.block_tables, ctx.cu_seqlens_k, total)
+        for layer in range(L):
+            kc, vc = cache[0, layer], cache[1, layer]
+            s0 = store_timer.start() if store_timer else None
+            backend.store(new_k[layer], new_v[layer], kc, vc, ctx.slot_mapping)
+            if store_timer:
+                store_timer.stop(s0)
+            t0 = timer.start() if timer else None
+            backend.gather_varlen(kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
+                                  plan=plan, out=(k_out, v_out))
+            if timer:
+                timer.stop(t0)
+        return ctx
+
+    # ---------------------------------------------------------- correctness gate
+    check_layers = [int(x) for x in args.check_layers.split(",") if x.strip()] if not args.profile else []
+    if check_layers:
+        from oracle import c_oracle
+
+        tables = wl.padded_block_tables()
+        used = np.unique(tables[tables >= 0])
+        remap = np.full(wl.num_blocks, -1, np.int64)
+        remap[used] = np.arange(used.size)
+        index = torch.from_numpy(used.astype(np.int64)).to(device)
+        ctables = np.where(tables >= 0, remap[np.maximum(tables, 0)], -1).astype(np.int32)
+        cslots = (remap[wl.slot_mapping // wl.block_size] * wl.block_size
+                  + wl.slot_mapping % wl.block_size).astype(np.int32)
+        before = {}
+        for layer in check_layers:
+            before[layer] = [cache[kv, layer].index_select(0, index).cpu().view(torch.int16).numpy()
+                             for kv in range(2)]
+        ctx = packer.pack_decode(batch)
+        plan = backend.build_gather_plan(cache[0, 0], ctx.block_tables, ctx.cu_seqlens_k, total)
+        cu = wl.cu_seqlens_k()
+        for layer in range(L):
+            kc, vc = cache[0, layer], cache[1, layer]
+            backend.store(new_k[layer], new_v[layer], kc, vc, ctx.slot_mapping)
+            backend.gather_varlen(kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
+                                  plan=plan, out=(k_out, v_out))
+            if layer in before:
+                hk, hv = before[layer]
+                c_oracle.store(wl.key[layer].view(torch.int16).numpy(),
+                               wl.value[layer].view(torch.int16).numpy(), hk, hv, cslots,
+                               threads=c_oracle.default_threads())
+                for got, host in ((k_out, hk), (v_out, hv)):
+                    expected = c_oracle.gather_varlen(host, ctables, cu, threads=c_oracle.default_threads())
+                    if not np.array_equal(got.cpu().view(torch.int16).numpy(), expected):
+                        raise AssertionError(f"decode step layer {layer}: gather differs from the oracle")
+                log(f"[bench] correctness gate: layer {layer} store+gather bit-exact vs oracle")
+        torch.cuda.synchronize()
+
+    # -------------------------------------------------------------- timed steps
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = LaunchTimer(stream)
+    store_timer = LaunchTimer(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start_evt = torch.cuda.Event(enable_timing=True)
+    end_evt = torch.cuda.Event(enable_timing=True)
+    start_evt.record(stream)
+    for _ in range(args.steps):
+        step(timer, store_timer)
+    end_evt.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    step_ms = start_evt.elapsed_time(end_evt) / args.steps
+    log(f"[bench] {args.steps} steps: {step_ms:.3f} ms/step (wall {wall_s * 1000 / args.steps:.3f})")
+
+    store_bytes = wl.store_bytes()
+    gather_bytes = wl.gather_bytes()
+    step_bytes = store_bytes + gather_bytes
+    gbps = step_bytes / (step_ms * 1e-3) / 1e9
+    gather_launch_bytes = wl.gather_bytes(layers=1)
+    gather_us = timer.durations_us()
+    store_us = store_timer.durations_us()
+    gather_mean = sum(gather_us) / len(gather_us)
+    achieved = gather_launch_bytes / (gather_mean * 1e-6) / 1e9
+
+    traffic = None
+    if TRAFFIC_FILE.is_file():
+        try:
+            t = json.loads(TRAFFIC_FILE.read_text())
+            if t.get("workload") == "decode_step" and t.get("layers_per_launch") == 1:
+                traffic = t.get("bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    cpu_baseline = None
+    if not args.profile and args.cpu_baseline_layers > 0:
+        cpu_baseline = run_cpu_baseline(wl, args.cpu_baseline_layers, args.cpu_baseline_repeats)
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "continuous-batching decode step, Qwen3-VL-2B LM KV shape",
+            "layers": L,
+            "live_sequences": B,
+            "context_tokens": total,
+            "context_law": "log-uniform [256, 16384], 16 evicted + 16 admitted",
+            "kv_heads": wl.num_kv_heads,
+            "head_dim": wl.head_dim,
+            "block_size": wl.block_size,
+            "num_blocks": wl.num_blocks,
+            "cache_bytes": int(cache.numel() * cache.element_size()),
+            "parallelism": "single GPU",
+        },
+        "hbm_fraction": round(gbps / MI355X_HBM_PEAK_GBPS, 4),
+        "decode_tokens_per_s": round(B / (step_ms * 1e-3), 2),
+        "step_bytes": step_bytes,
+        "reference_effective_bytes_per_step": L * (
+            effective_bytes("store", B, wl.num_kv_heads, wl.head_dim, 2)
+            + 2 * effective_bytes("gather", total, wl.num_kv_heads, wl.head_dim, 2)),
+        "kernels": {
+            "gather_varlen_planned_us": summarize_latencies(gather_us),
+            "store_us": summarize_latencies(store_us),
+        },
+        "roofline": {
+            "kernel": "gather_planned_kernel (K+V varlen gather, one layer)",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": MI355X_HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / MI355X_HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": gather_launch_bytes,
+        },
+        "cpu_baseline": cpu_baseline,
+        "host": {"platform": platform.platform(), "torch": torch.__version__, "hip": torch.version.hip,
+                 "gpu": torch.cuda.get_device_name(device)},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def run_cpu_baseline(wl, layers: int, repeats: int) -> dict:
+    """The oracle's C restatement (OpenMP) on the host cores: one decode
+    step of ``layers`` layers (pack, then per layer store + K/V varlen
+    gather) against ONE layer-sized host cache reused by every layer (the
+    full cache does not fit host memory), bytes counted as on the GPU."""
+    import numpy as np
+    import torch
+
+    from oracle import c_oracle
+
+    threads = c_oracle.default_threads()
+    kc = np.full((wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim), 0x3F80, dtype=np.int16)
+    vc = np.full_like(kc, 0x3F80)
+    tables = wl.padded_block_tables()
+    offsets, ids = wl.csr()
+    total = int(wl.num_tokens.sum())
+    k_out = np.empty((total, wl.num_kv_heads, wl.head_dim), dtype=np.int16)
+    v_out = np.empty_like(k_out)
+    keys = wl.key.view(torch.int16).numpy()
+    values = wl.value.view(torch.int16).numpy()
+
+    def cpu_step():
+        packed = c_oracle.pack_decode(wl.num_tokens, offsets, ids, wl.block_size, tables.shape[1])
+        for layer in range(layers):
+            c_oracle.store(keys[layer % keys.shape[0]], values[layer % values.shape[0]], kc, vc,
+                           packed["slot_mapping"], threads=threads)
+            c_oracle.gather_varlen(kc, packed["block_tables"], packed["cu_seqlens_k"], threads=threads, out=k_out)
+            c_oracle.gather_varlen(vc, packed["block_tables"], packed["cu_seqlens_k"], threads=threads, out=v_out)
+
+    cpu_step()  # first touch of the outputs
+    times = []
+    for _ in range(max(1, repeats)):
+        t0 = time.perf_counter()
+        cpu_step()
+        times.append(time.perf_counter() - t0)
+    seconds = sorted(times)[len(times) // 2]
+    step_bytes = wl.store_bytes(layers=layers) + wl.gather_bytes(layers=layers)
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(step_bytes / seconds / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle C restatement (OpenMP, {threads} threads): pack + {layers} layers of "
+                   f"store + K/V varlen gather of the same decode step against one layer-sized "
+                   f"host cache, median of {max(1, repeats)} runs, {seconds:.2f} s each"),
+        "decode_tokens_per_s_equivalent": round(wl.num_seqs / (seconds * wl.num_layers / layers), 2),
+        "cpu_model": model,
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

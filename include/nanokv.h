@@ -1,0 +1,233 @@
+/*
+ * nanokv — paged KV-cache store / gather / ragged-batch metadata packing for
+ * AMD Instinct MI355X (gfx950).  Plain C ABI: device pointers, int64 sizes,
+ * an opaque stream handle (a hipStream_t; NULL = the legacy default stream).
+ *
+ * Every entry point is asynchronous on `stream`, returns 0 on success and a
+ * non-zero NKV_E* code on failure; nkv_last_error() then returns a message
+ * (thread-local, valid until the next call on the same thread).  Contract
+ * violations that the host can see without reading device memory (negative
+ * sizes, misaligned pointers for the dtype, capacity too small) are rejected
+ * before any launch.  Index VALUES living in device memory (slots, physical
+ * block ids) are never trusted by the kernels: a slot outside [0, num_slots)
+ * is skipped like the -1 padding slot, and a physical block outside
+ * [0, num_blocks) yields zero-filled output rows, so a bad index can never
+ * fault the GPU.  Range validation that raises is the host's job (the Python
+ * validators, behind NANOVLLM_PAGED_KV_VALIDATE_INDICES as in the reference).
+ *
+ * Layouts (all row-major / contiguous unless a stride says otherwise):
+ *   cache         [num_blocks, block_size, kv_heads, head_dim]; one "row" is
+ *                 one (block, slot) = row_elems = kv_heads*head_dim elements.
+ *   key / value   [num_tokens, kv_heads, head_dim] with an arbitrary token
+ *                 stride (fused-QKV views) and contiguous inner dims.
+ *   block_tables  [num_seqs, table_stride] int32, -1 padded, contiguous
+ *                 (table_stride is both the row stride and the width).
+ *   cu_seqlens    [num_seqs + 1] int32 exclusive prefix sums.
+ *
+ * dtype selects only the element size (the kernels move bits, never convert).
+ */
+#ifndef NANOKV_H
+#define NANOKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes: the three dtypes the reference dispatches on
+ * (AT_DISPATCH_FLOATING_TYPES_AND2(Half, BFloat16) in
+ * csrc/paged_kv/paged_kv_cuda.cu:115-117 and :149-151). */
+#define NKV_DTYPE_FLOAT16 0
+#define NKV_DTYPE_BFLOAT16 1
+#define NKV_DTYPE_FLOAT32 2
+
+/* error codes */
+#define NKV_OK 0
+#define NKV_E_INVALID 1   /* bad argument (host-visible contract violation) */
+#define NKV_E_HIP 2       /* a HIP runtime call failed                      */
+#define NKV_E_CAPACITY 3  /* caller buffer / limit too small                */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int nkv_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* nkv_last_error(void);
+
+/*
+ * Store: for every token t with 0 <= slot_mapping[t] < num_slots, copy the
+ * key row t into key_cache row slot_mapping[t] and the value row t into
+ * value_cache row slot_mapping[t]; slot -1 (and any other out-of-range slot)
+ * is skipped.  num_tokens == 0 is a no-op.
+ *
+ * Replaces: the op `nanovllm_paged_kv::store(Tensor key, Tensor value,
+ *   Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor slot_mapping) -> ()`
+ *   (csrc/paged_kv/paged_kv.cpp:200-201), whose CUDA implementation is
+ *   store_cuda (csrc/paged_kv/paged_kv_cuda.cu:96-132); semantics of the
+ *   pytorch oracle nanovllm/layers/paged_kv/pytorch_backend.py:26-38.
+ * Strides are in elements (key.stride(0), value.stride(0)); row_elems is
+ * kv_heads*head_dim (key.size(1)*key.size(2)); num_slots is
+ * num_blocks*block_size of the cache.
+ */
+int nkv_store(const void* key, const void* value, void* key_cache,
+              void* value_cache, const int32_t* slot_mapping,
+              int64_t num_tokens, int64_t key_token_stride,
+              int64_t value_token_stride, int64_t row_elems,
+              int64_t num_slots, int32_t dtype, void* stream);
+
+/*
+ * Gather one sequence: out[t] = cache row (block_table[t / block_size],
+ * t % block_size) for t in [0, sequence_length).  out is a contiguous
+ * [sequence_length, row_elems] buffer owned by the caller.
+ *
+ * Replaces: the op `nanovllm_paged_kv::gather(Tensor cache,
+ *   Tensor block_table, int sequence_length) -> Tensor`
+ *   (csrc/paged_kv/paged_kv.cpp:202), CUDA implementation gather_cuda
+ *   (csrc/paged_kv/paged_kv_cuda.cu:134-164); pytorch oracle
+ *   nanovllm/layers/paged_kv/pytorch_backend.py:40-50.  The output
+ *   allocation the reference op performs (at::empty, :142-143) is done by
+ *   the caller here, so the ABI never allocates.  table_len (entries of
+ *   block_table) must cover ceil(sequence_length / block_size) blocks, the
+ *   check of nanovllm/layers/paged_kv/base.py:138-139.
+ */
+int nkv_gather(const void* cache, const int32_t* block_table,
+               int64_t table_len, int64_t sequence_length, int64_t block_size,
+               int64_t row_elems, int64_t num_blocks, int32_t dtype,
+               void* out, void* stream);
+
+/*
+ * Gather plans.  A plan splits every sequence's context into chunks of
+ * `chunk_rows` consecutive rows that never cross a cache block, one int4
+ * entry {src_row, dst_row, num_rows, seq} per chunk; it depends only on the
+ * block tables and cu_seqlens_k, so one plan serves both caches of every
+ * layer in a decode step.  Entries past the real chunk count have
+ * num_rows = 0.  src_row = -1 marks a chunk whose physical block is outside
+ * [0, num_blocks) (rows come out zero-filled).
+ *
+ * nkv_gather_plan_rows: the chunk length (rows) the library uses for a row
+ *   size and block size (a divisor of block_size).
+ * nkv_gather_plan_capacity: entries needed for total_rows rows spread over
+ *   num_seqs sequences (an upper bound, ceil(total_rows/chunk)+num_seqs).
+ */
+int64_t nkv_gather_plan_rows(int64_t block_size, int64_t row_elems,
+                             int32_t dtype);
+int64_t nkv_gather_plan_capacity(int64_t total_rows, int64_t num_seqs,
+                                 int64_t block_size, int64_t row_elems,
+                                 int32_t dtype);
+
+/*
+ * Build a gather plan on the device from block_tables [num_seqs,
+ * table_stride] and cu_seqlens_k [num_seqs+1] (context lengths are
+ * cu_seqlens_k[i+1]-cu_seqlens_k[i]).  plan must hold `capacity` int4
+ * entries (16 B each, 16-B aligned); capacity must be at least
+ * nkv_gather_plan_capacity(cu_seqlens_k[num_seqs], ...).  num_seqs is
+ * limited to NKV_MAX_PLAN_SEQS.  out_rows is the row count of the outputs
+ * the plan will be used with: chunks outside [0, out_rows) are clipped, and
+ * a logical block at or past table_stride reads as invalid, so wrong
+ * device-side lengths cannot make the gather write or read out of bounds.
+ *
+ * No reference counterpart as a single call: it replaces the per-request
+ * host loop of SDPAAttention (nanovllm/layers/attention.py:250-259 prefill,
+ * :284-292 decode) that issues one gather launch per (request, K or V).
+ */
+#define NKV_MAX_PLAN_SEQS 8192
+int nkv_build_gather_plan(const int32_t* block_tables, int64_t table_stride,
+                          const int32_t* cu_seqlens_k, int64_t num_seqs,
+                          int64_t out_rows, int64_t block_size, int64_t row_elems,
+                          int64_t num_blocks, int32_t dtype, void* plan,
+                          int64_t capacity, void* stream);
+
+/*
+ * Varlen gather of K and V for every sequence with one launch, driven by a
+ * plan from nkv_build_gather_plan (same block_size/row_elems/dtype):
+ * key_out[cu_seqlens_k[i] + t] = key_cache row of token t of sequence i,
+ * likewise for V.  Equals, byte for byte, the concatenation over i of the
+ * reference's gather(cache, block_tables[i], context_len[i])
+ * (nanovllm/layers/attention.py:254-259, :287-292).
+ * value_cache / value_out may be NULL together to gather one cache only.
+ * cache_rows (num_blocks*block_size of each cache) and out_rows (rows of
+ * each output) bound every entry: an entry reaching past the cache is
+ * zero-filled, one reaching past the output is skipped, so the launch stays
+ * in bounds whatever plan it is given.
+ */
+int nkv_gather_varlen_planned(const void* key_cache, const void* value_cache,
+                              const void* plan, int64_t capacity,
+                              int64_t cache_rows, int64_t out_rows,
+                              int64_t row_elems, int32_t dtype,
+                              void* key_out, void* value_out, void* stream);
+
+/*
+ * Convenience: build the plan into `workspace` (workspace_bytes >=
+ * 16*capacity) and run the planned gather, two launches.
+ */
+int nkv_gather_varlen(const void* key_cache, const void* value_cache,
+                      const int32_t* block_tables, int64_t table_stride,
+                      const int32_t* cu_seqlens_k, int64_t num_seqs,
+                      int64_t total_rows, int64_t block_size,
+                      int64_t row_elems, int64_t num_blocks, int32_t dtype,
+                      void* key_out, void* value_out, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/*
+ * Decode-step metadata packing on the device.  Input is the scheduler's
+ * per-sequence state in CSR form: num_tokens[i] (len(seq)), and the block
+ * list of sequence i = block_ids[block_offsets[i] .. block_offsets[i+1]);
+ * num_block_ids is the length of block_ids (reads past it yield -1).
+ * Outputs (all int32, device):
+ *   slot_mapping[i]  = last_block*block_size + last_block_num_tokens - 1
+ *                      (-1 when the block list is empty)
+ *   context_lens[i]  = num_tokens[i]
+ *   block_tables     [num_seqs, table_width], -1 padded; table_width must
+ *                    be >= the longest block list
+ *   cu_seqlens_k     [num_seqs+1], exclusive prefix sum of num_tokens
+ *                    (may be NULL)
+ *
+ * Replaces: ModelRunner.prepare_decode's host loop and copies
+ *   (nanovllm/engine/model_runner.py:892-938), the slot formula with
+ *   Sequence.last_block_num_tokens (nanovllm/engine/sequence.py:176-183)
+ *   and prepare_block_tables (model_runner.py:696-707).
+ */
+#define NKV_MAX_PACK_SEQS 4096
+int nkv_pack_decode(const int32_t* num_tokens, const int32_t* block_offsets,
+                    const int32_t* block_ids, int64_t num_block_ids,
+                    int64_t num_seqs,
+                    int64_t block_size, int64_t table_width,
+                    int32_t* slot_mapping, int32_t* context_lens,
+                    int32_t* block_tables, int32_t* cu_seqlens_k,
+                    void* stream);
+
+/*
+ * Prefill / chunked-prefill metadata packing on the device.  Per sequence:
+ * start = num_cached[i], q = num_scheduled[i], end = start + q.
+ *   cu_seqlens_q    [num_seqs+1]  exclusive scan of q
+ *   cu_seqlens_k    [num_seqs+1]  exclusive scan of end
+ *   slot_mapping    [num_slots]   for every sequence with a non-empty block
+ *                                 list, in order, the slots of positions
+ *                                 start..end-1:
+ *                                 bt[p / block_size]*block_size + p % block_size;
+ *                                 sequences with an empty block list emit
+ *                                 nothing.  num_slots must equal that total.
+ *   block_tables    [num_seqs, table_width] -1 padded (may be NULL)
+ *   full_context_lens[i] = num_prompt[i]   (may be NULL with num_prompt)
+ *   query_start_lens[i]  = start           (may be NULL)
+ *   max_seqlens[0..1]    = max q, max end  (may be NULL)
+ *
+ * Replaces: ModelRunner.prepare_prefill's metadata part
+ *   (nanovllm/engine/model_runner.py:757-820, 856-882).
+ */
+int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
+                     const int32_t* num_prompt, const int32_t* block_offsets,
+                     const int32_t* block_ids, int64_t num_block_ids,
+                     int64_t num_seqs,
+                     int64_t block_size, int64_t table_width,
+                     int64_t num_slots, int32_t* cu_seqlens_q,
+                     int32_t* cu_seqlens_k, int32_t* slot_mapping,
+                     int32_t* block_tables, int32_t* full_context_lens,
+                     int32_t* query_start_lens, int32_t* max_seqlens,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOKV_H */

@@ -1,0 +1,107 @@
+"""ctypes binding of ``libnanokv.so`` (the C ABI of ``include/nanokv.h``).
+
+The library is loaded lazily, once, under a lock (the double-checked load of
+the reference's CUDA backend, nanovllm/layers/paged_kv/cuda_backend.py:21-42).
+A missing or unloadable library raises ``RuntimeError`` with the path and the
+loader's message: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from threading import Lock
+
+from nanokv.build import LIBRARY_PATH
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_ptr = ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/nanokv.h.
+SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
+    "nkv_version": (ctypes.c_int, ()),
+    "nkv_last_error": (ctypes.c_char_p, ()),
+    "nkv_store": (
+        ctypes.c_int,
+        (c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_ptr),
+    ),
+    "nkv_gather": (
+        ctypes.c_int,
+        (c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_ptr, c_ptr),
+    ),
+    "nkv_gather_plan_rows": (c_i64, (c_i64, c_i64, c_i32)),
+    "nkv_gather_plan_capacity": (c_i64, (c_i64, c_i64, c_i64, c_i64, c_i32)),
+    "nkv_build_gather_plan": (
+        ctypes.c_int,
+        (c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_ptr, c_i64, c_ptr),
+    ),
+    "nkv_gather_varlen_planned": (
+        ctypes.c_int,
+        (c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr),
+    ),
+    "nkv_gather_varlen": (
+        ctypes.c_int,
+        (
+            c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64,
+            c_i32, c_ptr, c_ptr, c_ptr, c_i64, c_ptr,
+        ),
+    ),
+    "nkv_pack_decode": (
+        ctypes.c_int,
+        (c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr),
+    ),
+    "nkv_pack_prefill": (
+        ctypes.c_int,
+        (
+            c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64,
+            c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+        ),
+    ),
+}
+
+NKV_DTYPE_FLOAT16 = 0
+NKV_DTYPE_BFLOAT16 = 1
+NKV_DTYPE_FLOAT32 = 2
+NKV_MAX_PLAN_SEQS = 8192
+NKV_MAX_PACK_SEQS = 4096
+
+_LOCK = Lock()
+_LIBRARY: ctypes.CDLL | None = None
+
+
+def library_path() -> str:
+    return str(LIBRARY_PATH)
+
+
+def load_library() -> ctypes.CDLL:
+    """Return the loaded library, loading it on first use."""
+    global _LIBRARY
+    if _LIBRARY is not None:
+        return _LIBRARY
+    with _LOCK:
+        if _LIBRARY is None:
+            if not LIBRARY_PATH.is_file():
+                raise RuntimeError(
+                    f"nanokv HIP library not built: {LIBRARY_PATH} is missing "
+                    "(run __graft_entry__.build() or python -m nanokv.build)"
+                )
+            try:
+                library = ctypes.CDLL(str(LIBRARY_PATH))
+            except OSError as exc:
+                raise RuntimeError(f"failed to load {LIBRARY_PATH}: {exc}") from exc
+            for name, (restype, argtypes) in SIGNATURES.items():
+                try:
+                    function = getattr(library, name)
+                except AttributeError as exc:
+                    raise RuntimeError(f"{LIBRARY_PATH} does not export {name}") from exc
+                function.restype = restype
+                function.argtypes = list(argtypes)
+            _LIBRARY = library
+    return _LIBRARY
+
+
+def check(status: int, what: str) -> None:
+    """Raise RuntimeError carrying nkv_last_error() when status != 0."""
+    if status != 0:
+        message = load_library().nkv_last_error()
+        text = message.decode("utf-8", "replace") if message else ""
+        raise RuntimeError(f"{what} failed (nkv status {status}): {text}")

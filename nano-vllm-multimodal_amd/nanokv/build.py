@@ -1,0 +1,96 @@
+"""Build recipe for ``libnanokv.so``: the HIP kernels plus the C ABI declared
+in ``include/nanokv.h``, compiled with hipcc for gfx950 into this package
+directory (in-tree, so the library travels with the source tree).
+
+Run ``python -m nanokv.build`` (with ``nano-vllm-multimodal_amd`` on
+``sys.path``) or call :func:`build`.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+SOURCE_DIR = PACKAGE_DIR.parent / "csrc"
+INCLUDE_DIR = PACKAGE_DIR.parents[1] / "include"
+LIBRARY_PATH = PACKAGE_DIR / "libnanokv.so"
+SOURCES = ("nkv_api.hip", "nkv_store.hip", "nkv_gather.hip", "nkv_pack.hip")
+OFFLOAD_ARCH = "gfx950"
+HIPCC_FLAGS = (
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Wall",
+    # Packed FP32 instructions are kept out of every code object.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+)
+
+
+def hipcc_path() -> str:
+    candidates = []
+    rocm = os.environ.get("ROCM_PATH") or os.environ.get("HIP_PATH")
+    if rocm:
+        candidates.append(Path(rocm) / "bin" / "hipcc")
+    candidates.append(Path("/opt/rocm/bin/hipcc"))
+    for candidate in candidates:
+        if candidate.is_file() and os.access(candidate, os.X_OK):
+            return str(candidate)
+    found = shutil.which("hipcc")
+    if found:
+        return found
+    raise RuntimeError("hipcc not found (set ROCM_PATH); cannot build libnanokv.so")
+
+
+def build_command(output: Path) -> list[str]:
+    return [
+        hipcc_path(),
+        *HIPCC_FLAGS,
+        f"-I{INCLUDE_DIR}",
+        *(str(SOURCE_DIR / name) for name in SOURCES),
+        "-o",
+        str(output),
+    ]
+
+
+def build(*, verbose: bool = False) -> Path:
+    """Compile the library (always, even if a build exists) and install it
+    atomically at :data:`LIBRARY_PATH`."""
+    missing = [name for name in SOURCES if not (SOURCE_DIR / name).is_file()]
+    if missing:
+        raise RuntimeError(f"nanokv sources missing: {', '.join(missing)}")
+    with tempfile.TemporaryDirectory(prefix="nanokv-build-") as tmp:
+        output = Path(tmp) / LIBRARY_PATH.name
+        command = build_command(output)
+        if verbose:
+            print(" ".join(command), flush=True)
+        result = subprocess.run(command, capture_output=True, text=True)
+        diagnostics = "\n".join(
+            line
+            for line in (result.stdout + result.stderr).splitlines()
+            # The host pass does not know the GPU target feature; harmless.
+            if "packed-fp32-ops" not in line
+        ).strip()
+        if result.returncode != 0:
+            raise RuntimeError(
+                f"hipcc failed ({result.returncode}) building libnanokv.so:\n{diagnostics}"
+            )
+        if diagnostics and verbose:
+            print(diagnostics, flush=True)
+        staged = LIBRARY_PATH.with_name(LIBRARY_PATH.name + ".tmp")
+        shutil.copyfile(output, staged)
+        os.replace(staged, LIBRARY_PATH)
+    return LIBRARY_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

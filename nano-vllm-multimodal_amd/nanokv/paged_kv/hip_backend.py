@@ -1,0 +1,209 @@
+"""The ``hip`` paged-KV backend: the reference's backend protocol
+(nanovllm/layers/paged_kv/base.py:38-65) implemented by the nanokv HIP
+library for MI355X.
+
+It mirrors the reference's CUDA backend (nanovllm/layers/paged_kv/
+cuda_backend.py:31-104): validate with the shared validators, then call the
+``nanovllm_paged_kv`` ops.  Loading is lazy and lock-protected; a missing
+library raises instead of falling back to another backend.
+"""
+from __future__ import annotations
+
+from threading import Lock
+from typing import Sequence
+
+import torch
+
+from nanokv import _lib
+from nanokv.paged_kv import ops
+from nanokv.paged_kv.base import (
+    PagedKVAllocation,
+    validate_gather_inputs,
+    validate_store_inputs,
+)
+
+_LOAD_LOCK = Lock()
+_READY = False
+
+
+def hip_runtime_available() -> bool:
+    """True on a ROCm build of PyTorch with a visible GPU."""
+    return torch.version.hip is not None and torch.cuda.is_available()
+
+
+def hip_extension_available() -> bool:
+    """True when the built library loads and exports the full ABI."""
+    try:
+        _lib.load_library()
+    except RuntimeError:
+        return False
+    return True
+
+
+def reset_hip_backend_state_for_tests() -> None:
+    global _READY
+    with _LOAD_LOCK:
+        _READY = False
+
+
+class HIPPagedKVBackend:
+    name = "hip"
+
+    @staticmethod
+    def _load() -> None:
+        global _READY
+        if _READY:
+            return
+        with _LOAD_LOCK:
+            if not _READY:
+                _lib.load_library()
+                ops.register_ops()
+                _READY = True
+
+    def allocate(
+        self,
+        shape: Sequence[int],
+        *,
+        dtype: torch.dtype,
+        device: torch.device | str,
+    ) -> PagedKVAllocation:
+        """One device tensor for the whole [2, layers, blocks, block, heads,
+        dim] cache (model_runner.py:657-674); per-layer views of it are
+        contiguous, which the kernels require."""
+        resolved = torch.device(device)
+        if resolved.type != "cuda":
+            raise ValueError("HIP Paged KV allocation requires a ROCm (cuda) device")
+        if dtype not in ops.DTYPE_CODES:
+            raise ValueError(f"HIP Paged KV allocation does not support dtype {dtype}")
+        if any(int(size) <= 0 for size in shape) or not shape:
+            raise ValueError("HIP Paged KV allocation dimensions must be positive")
+        self._load()
+        return PagedKVAllocation(torch.empty(tuple(int(s) for s in shape), dtype=dtype, device=resolved))
+
+    def store(
+        self,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        key_cache: torch.Tensor,
+        value_cache: torch.Tensor,
+        slot_mapping: torch.Tensor,
+    ) -> None:
+        validate_store_inputs(key, value, key_cache, value_cache, slot_mapping)
+        if not key.is_cuda:
+            raise ValueError("HIP Paged KV Store requires ROCm device tensors")
+        self._load()
+        torch.ops.nanovllm_paged_kv.store(key, value, key_cache, value_cache, slot_mapping)
+
+    def gather(
+        self,
+        cache: torch.Tensor,
+        block_table: torch.Tensor,
+        sequence_length: int,
+    ) -> torch.Tensor:
+        validate_gather_inputs(cache, block_table, sequence_length)
+        if not cache.is_cuda:
+            raise ValueError("HIP Paged KV Gather requires ROCm device tensors")
+        self._load()
+        return torch.ops.nanovllm_paged_kv.gather(cache, block_table, sequence_length)
+
+    def gather_varlen(
+        self,
+        key_cache: torch.Tensor,
+        value_cache: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_k: torch.Tensor,
+        total_tokens: int,
+        *,
+        plan: torch.Tensor | None = None,
+        out: tuple[torch.Tensor, torch.Tensor] | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """K and V of every sequence in one launch: rows
+        [cu_seqlens_k[i], cu_seqlens_k[i+1]) of the outputs equal
+        ``gather(cache, block_tables[i], cu_seqlens_k[i+1]-cu_seqlens_k[i])``
+        (the per-request loop of attention.py:250-259, 284-292).
+        ``total_tokens`` must equal ``cu_seqlens_k[-1]``.  A ``plan`` from
+        :meth:`build_gather_plan` (e.g. one per decode step, shared by all
+        layers) skips the planning launch; ``out`` reuses output buffers."""
+        validate_varlen_inputs(key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens)
+        self._load()
+        if plan is None and out is None:
+            return torch.ops.nanovllm_paged_kv.gather_varlen(
+                key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens
+            )
+        if plan is None:
+            plan = self.build_gather_plan(key_cache, block_tables, cu_seqlens_k, total_tokens)
+        if out is None:
+            key_out = torch.empty(
+                (total_tokens, *key_cache.shape[2:]), dtype=key_cache.dtype, device=key_cache.device
+            )
+            out = (key_out, torch.empty_like(key_out))
+        key_out, value_out = out
+        if key_out.shape[0] < total_tokens or value_out.shape != key_out.shape:
+            raise ValueError("varlen Gather outputs must hold total_tokens rows")
+        torch.ops.nanovllm_paged_kv.gather_varlen_planned(
+            key_cache, value_cache, plan, key_out, value_out
+        )
+        return key_out, value_out
+
+    def build_gather_plan(
+        self,
+        cache: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_k: torch.Tensor,
+        total_tokens: int,
+    ) -> torch.Tensor:
+        """Chunk list for :meth:`gather_varlen`; valid for every cache with
+        the shape and dtype of ``cache`` (all layers, K and V)."""
+        self._load()
+        num_blocks, block_size, heads, head_dim = cache.shape
+        return torch.ops.nanovllm_paged_kv.build_gather_plan(
+            block_tables, cu_seqlens_k, total_tokens, num_blocks, block_size,
+            heads * head_dim, cache.dtype,
+        )
+
+
+def validate_varlen_inputs(
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    total_tokens: int,
+) -> None:
+    """Host-visible contract of gather_varlen, in the style of
+    base.py:117-151: shapes, dtypes and devices always; index values only
+    when index validation is enabled (it synchronises)."""
+    if key_cache.ndim != 4 or key_cache.shape != value_cache.shape:
+        raise ValueError("key and value cache shape must match [blocks, block, kv_heads, head_dim]")
+    if key_cache.dtype != value_cache.dtype:
+        raise ValueError("key and value caches must have matching dtype")
+    if block_tables.dtype != torch.int32 or block_tables.ndim != 2:
+        raise ValueError("block_tables must be a two-dimensional int32 tensor")
+    if not block_tables.is_contiguous():
+        raise ValueError("block_tables must be contiguous")
+    if cu_seqlens_k.dtype != torch.int32 or cu_seqlens_k.ndim != 1 or not cu_seqlens_k.is_contiguous():
+        raise ValueError("cu_seqlens_k must be a contiguous one-dimensional int32 tensor")
+    if cu_seqlens_k.numel() != block_tables.shape[0] + 1:
+        raise ValueError("cu_seqlens_k must have one entry more than block_tables has rows")
+    devices = {t.device for t in (key_cache, value_cache, block_tables, cu_seqlens_k)}
+    if len(devices) != 1:
+        raise ValueError("all paged KV Gather tensors must be on the same device")
+    if total_tokens < 0:
+        raise ValueError("total_tokens must be non-negative")
+    if not key_cache.is_cuda:
+        raise ValueError("HIP Paged KV Gather requires ROCm device tensors")
+    from nanokv.paged_kv.base import index_value_validation_enabled
+
+    if cu_seqlens_k.numel() and index_value_validation_enabled(cu_seqlens_k):
+        cu = cu_seqlens_k.cpu()
+        lengths = cu[1:] - cu[:-1]
+        if int(cu[0]) != 0 or bool((lengths < 0).any()) or int(cu[-1]) != total_tokens:
+            raise ValueError("cu_seqlens_k must start at 0, be non-decreasing and end at total_tokens")
+        block_size, num_blocks = key_cache.shape[1], key_cache.shape[0]
+        needed = (lengths + block_size - 1) // block_size
+        if bool((needed > block_tables.shape[1]).any()):
+            raise ValueError("block_tables do not cover the requested sequence lengths")
+        tables = block_tables.cpu()
+        columns = torch.arange(tables.shape[1]).unsqueeze(0)
+        used = columns < needed.unsqueeze(1)
+        if bool((((tables < 0) | (tables >= num_blocks)) & used).any()):
+            raise ValueError("block_tables contain an invalid physical block")

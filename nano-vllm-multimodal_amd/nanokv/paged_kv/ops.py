@@ -1,0 +1,233 @@
+"""``torch.library`` registration of the paged-KV ops, implemented by the
+HIP library through its C ABI.
+
+Namespace and the two reference schemas are unchanged
+(csrc/paged_kv/paged_kv.cpp:199-203):
+
+    nanovllm_paged_kv::store(Tensor key, Tensor value, Tensor(a!) key_cache,
+                             Tensor(b!) value_cache, Tensor slot_mapping) -> ()
+    nanovllm_paged_kv::gather(Tensor cache, Tensor block_table,
+                              int sequence_length) -> Tensor
+
+The implementations sit on the CUDA dispatch key, the key ROCm device
+tensors carry under PyTorch-ROCm (the reference registers its kernels there
+too, paged_kv_cuda.cu:168-171).  Additive ops, with no reference schema:
+
+    gather_varlen(Tensor key_cache, Tensor value_cache, Tensor block_tables,
+                  Tensor cu_seqlens_k, int total_tokens) -> (Tensor, Tensor)
+    build_gather_plan(Tensor block_tables, Tensor cu_seqlens_k,
+                      int total_tokens, int num_blocks, int block_size,
+                      int row_elems, ScalarType dtype) -> Tensor
+    gather_varlen_planned(Tensor key_cache, Tensor value_cache, Tensor plan,
+                          Tensor(a!) key_out, Tensor(b!) value_out) -> ()
+
+Every kernel runs on the current stream of the tensors' device and returns
+before it completes, like the reference ops.
+"""
+from __future__ import annotations
+
+from threading import Lock
+
+import torch
+
+from nanokv import _lib
+
+NAMESPACE = "nanovllm_paged_kv"
+
+SCHEMAS = {
+    "store": "store(Tensor key, Tensor value, Tensor(a!) key_cache, "
+    "Tensor(b!) value_cache, Tensor slot_mapping) -> ()",
+    "gather": "gather(Tensor cache, Tensor block_table, int sequence_length) -> Tensor",
+    "gather_varlen": "gather_varlen(Tensor key_cache, Tensor value_cache, "
+    "Tensor block_tables, Tensor cu_seqlens_k, int total_tokens) -> (Tensor, Tensor)",
+    "build_gather_plan": "build_gather_plan(Tensor block_tables, Tensor cu_seqlens_k, "
+    "int total_tokens, int num_blocks, int block_size, int row_elems, "
+    "ScalarType dtype) -> Tensor",
+    "gather_varlen_planned": "gather_varlen_planned(Tensor key_cache, Tensor value_cache, "
+    "Tensor plan, Tensor(a!) key_out, Tensor(b!) value_out) -> ()",
+}
+
+DTYPE_CODES = {
+    torch.float16: _lib.NKV_DTYPE_FLOAT16,
+    torch.bfloat16: _lib.NKV_DTYPE_BFLOAT16,
+    torch.float32: _lib.NKV_DTYPE_FLOAT32,
+}
+
+_REGISTER_LOCK = Lock()
+_FRAGMENT: torch.library.Library | None = None
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise RuntimeError(
+            f"nanokv paged KV ops support float16, bfloat16 and float32, not {dtype}"
+        ) from None
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device(what: str, *tensors: torch.Tensor) -> torch.device:
+    device = tensors[0].device
+    for tensor in tensors:
+        if not tensor.is_cuda or tensor.device != device:
+            raise ValueError(f"{what} requires ROCm device tensors on one device")
+    return device
+
+
+def _require_contiguous_cache(what: str, *caches: torch.Tensor) -> None:
+    for cache in caches:
+        if not cache.is_contiguous():
+            raise ValueError(f"{what} requires contiguous [blocks, block, kv_heads, head_dim] caches")
+
+
+def _plan_capacity(total: int, num_seqs: int, block_size: int, row_elems: int, code: int) -> int:
+    return int(
+        _lib.load_library().nkv_gather_plan_capacity(total, num_seqs, block_size, row_elems, code)
+    )
+
+
+def _store_impl(key, value, key_cache, value_cache, slot_mapping) -> None:
+    device = _require_device("paged KV HIP Store", key, value, key_cache, value_cache, slot_mapping)
+    _require_contiguous_cache("paged KV HIP Store", key_cache, value_cache)
+    if key.dtype != value.dtype or key.dtype != key_cache.dtype or key.dtype != value_cache.dtype:
+        raise RuntimeError("Paged KV HIP Store dtype mismatch")
+    num_tokens = key.shape[0]
+    if num_tokens == 0:
+        return
+    library = _lib.load_library()
+    status = library.nkv_store(
+        key.data_ptr(),
+        value.data_ptr(),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        slot_mapping.data_ptr(),
+        num_tokens,
+        key.stride(0),
+        value.stride(0),
+        key.shape[1] * key.shape[2],
+        key_cache.shape[0] * key_cache.shape[1],
+        dtype_code(key.dtype),
+        _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::store")
+
+
+def _gather_impl(cache, block_table, sequence_length: int) -> torch.Tensor:
+    device = _require_device("paged KV HIP Gather", cache, block_table)
+    _require_contiguous_cache("paged KV HIP Gather", cache)
+    num_blocks, block_size, heads, head_dim = cache.shape
+    out = torch.empty((sequence_length, heads, head_dim), dtype=cache.dtype, device=device)
+    if sequence_length == 0:
+        return out
+    status = _lib.load_library().nkv_gather(
+        cache.data_ptr(),
+        block_table.data_ptr(),
+        block_table.numel(),
+        sequence_length,
+        block_size,
+        heads * head_dim,
+        num_blocks,
+        dtype_code(cache.dtype),
+        out.data_ptr(),
+        _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::gather")
+    return out
+
+
+def _build_plan_impl(
+    block_tables, cu_seqlens_k, total_tokens: int, num_blocks: int, block_size: int,
+    row_elems: int, dtype: torch.dtype,
+) -> torch.Tensor:
+    device = _require_device("paged KV HIP plan", block_tables, cu_seqlens_k)
+    num_seqs = cu_seqlens_k.numel() - 1
+    code = dtype_code(dtype)
+    capacity = _plan_capacity(total_tokens, num_seqs, block_size, row_elems, code)
+    plan = torch.empty((capacity, 4), dtype=torch.int32, device=device)
+    if capacity == 0:
+        return plan
+    status = _lib.load_library().nkv_build_gather_plan(
+        block_tables.data_ptr(),
+        block_tables.stride(0) if block_tables.ndim == 2 else 0,
+        cu_seqlens_k.data_ptr(),
+        num_seqs,
+        total_tokens,
+        block_size,
+        row_elems,
+        num_blocks,
+        code,
+        plan.data_ptr(),
+        capacity,
+        _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::build_gather_plan")
+    return plan
+
+
+def _gather_planned_impl(key_cache, value_cache, plan, key_out, value_out) -> None:
+    device = _require_device(
+        "paged KV HIP varlen Gather", key_cache, value_cache, plan, key_out, value_out
+    )
+    _require_contiguous_cache("paged KV HIP varlen Gather", key_cache, value_cache)
+    if plan.dtype != torch.int32 or plan.ndim != 2 or plan.shape[1] != 4 or not plan.is_contiguous():
+        raise ValueError("gather plan must be a contiguous [capacity, 4] int32 tensor")
+    if not (key_out.is_contiguous() and value_out.is_contiguous()):
+        raise ValueError("varlen Gather outputs must be contiguous")
+    if key_out.shape != value_out.shape or key_out.shape[1:] != key_cache.shape[2:]:
+        raise ValueError("varlen Gather outputs must be [rows, kv_heads, head_dim] of the caches")
+    if key_out.dtype != key_cache.dtype or value_out.dtype != key_cache.dtype:
+        raise ValueError("varlen Gather outputs must have the caches' dtype")
+    row_elems = key_cache.shape[2] * key_cache.shape[3]
+    status = _lib.load_library().nkv_gather_varlen_planned(
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        plan.data_ptr(),
+        plan.shape[0],
+        key_cache.shape[0] * key_cache.shape[1],
+        key_out.shape[0],
+        row_elems,
+        dtype_code(key_cache.dtype),
+        key_out.data_ptr(),
+        value_out.data_ptr(),
+        _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::gather_varlen_planned")
+
+
+def _gather_varlen_impl(key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens: int):
+    _require_device("paged KV HIP varlen Gather", key_cache, value_cache, block_tables, cu_seqlens_k)
+    num_blocks, block_size, heads, head_dim = key_cache.shape
+    key_out = torch.empty((total_tokens, heads, head_dim), dtype=key_cache.dtype, device=key_cache.device)
+    value_out = torch.empty_like(key_out)
+    if total_tokens == 0:
+        return key_out, value_out
+    plan = _build_plan_impl(
+        block_tables, cu_seqlens_k, total_tokens, num_blocks, block_size, heads * head_dim,
+        key_cache.dtype,
+    )
+    _gather_planned_impl(key_cache, value_cache, plan, key_out, value_out)
+    return key_out, value_out
+
+
+def register_ops() -> None:
+    """Define the schemas (unless another library already did) and register
+    the HIP implementations on the CUDA key.  Idempotent."""
+    global _FRAGMENT
+    with _REGISTER_LOCK:
+        if _FRAGMENT is not None:
+            return
+        fragment = torch.library.Library(NAMESPACE, "FRAGMENT")
+        namespace = getattr(torch.ops, NAMESPACE)
+        for name, schema in SCHEMAS.items():
+            if not hasattr(namespace, name):
+                fragment.define(schema)
+        fragment.impl("store", _store_impl, "CUDA")
+        fragment.impl("gather", _gather_impl, "CUDA")
+        fragment.impl("gather_varlen", _gather_varlen_impl, "CUDA")
+        fragment.impl("build_gather_plan", _build_plan_impl, "CUDA")
+        fragment.impl("gather_varlen_planned", _gather_planned_impl, "CUDA")
+        _FRAGMENT = fragment

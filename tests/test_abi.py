@@ -1,0 +1,80 @@
+"""CPU tests of the C ABI library: it is built for gfx950, loads without a
+GPU, exports every function include/nanokv.h declares, and rejects
+host-visible contract violations before any device work (these calls never
+reach the HIP runtime)."""
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from nanokv import _lib
+from nanokv.build import LIBRARY_PATH
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nanokv.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(nkv_[a-z_]+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    declared = declared_functions()
+    assert declared, "no declarations parsed"
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    assert LIBRARY_PATH.is_file(), "run __graft_entry__.build() first"
+    library = _lib.load_library()
+    declared = declared_functions()
+    for name in declared:
+        assert hasattr(library, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(LIBRARY_PATH)], capture_output=True, text=True)
+    exported = set(re.findall(r"\bT (nkv_[a-z_]+)\b", nm.stdout))
+    assert declared <= exported, declared - exported
+
+
+def test_library_carries_gfx950_code_object():
+    data = LIBRARY_PATH.read_bytes()
+    assert b"gfx950" in data
+
+
+def test_version_and_plan_geometry():
+    lib = _lib.load_library()
+    assert lib.nkv_version() >= 100
+    # chunk rows divide the block size and never exceed it
+    for block_size, row_elems, dtype in ((256, 1024, 1), (256, 256, 1), (16, 80, 2), (16, 15, 0), (4, 5, 0)):
+        rows = lib.nkv_gather_plan_rows(block_size, row_elems, dtype)
+        assert 1 <= rows <= block_size and block_size % rows == 0
+    assert lib.nkv_gather_plan_rows(256, 1024, 1) == 16  # 32 KiB chunks of 2 KiB rows
+    assert lib.nkv_gather_plan_rows(0, 1024, 1) == 0
+    assert lib.nkv_gather_plan_rows(256, 1024, 7) == 0
+    assert lib.nkv_gather_plan_capacity(1000, 4, 256, 1024, 1) == -(-1000 // 16) + 4
+    assert lib.nkv_gather_plan_capacity(0, 0, 256, 1024, 1) == 0
+
+
+@pytest.mark.parametrize("call,message", [
+    (lambda l: l.nkv_store(None, None, None, None, None, 1, 1, 1, 1, 1, 99, None), "dtype"),
+    (lambda l: l.nkv_store(None, None, None, None, None, -1, 1, 1, 1, 1, 1, None), "negative"),
+    (lambda l: l.nkv_store(None, None, None, None, None, 4, 8, 8, 8, 64, 1, None), "null"),
+    (lambda l: l.nkv_gather(None, None, 1, 5, 4, 8, 3, 1, None, None), "cover"),
+    (lambda l: l.nkv_gather(None, None, 2, -1, 4, 8, 3, 1, None, None), "non-negative"),
+    (lambda l: l.nkv_gather(None, None, 2, 5, 0, 8, 3, 1, None, None), "positive"),
+    (lambda l: l.nkv_build_gather_plan(None, 4, None, 9000, 10, 4, 8, 3, 1, None, 16, None), "num_seqs"),
+    (lambda l: l.nkv_gather_varlen_planned(None, None, None, 4, 8, 8, 8, 1, None, None, None), "null"),
+    (lambda l: l.nkv_gather_varlen(None, None, None, 1, None, 2, 100, 16, 8, 4, 1, None, None, None, 16, None), "workspace"),
+    (lambda l: l.nkv_pack_decode(None, None, None, 0, 5000, 16, 4, None, None, None, None, None), "num_seqs"),
+    (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 16, 4, None, None, None, None, None), "null"),
+    (lambda l: l.nkv_pack_prefill(None, None, None, None, None, 0, 3, 0, 4, 8, None, None, None, None, None, None, None, None), "block_size"),
+])
+def test_contract_violations_fail_before_launch(call, message):
+    lib = _lib.load_library()
+    status = call(lib)
+    assert status != 0
+    assert message in lib.nkv_last_error().decode()
+    with pytest.raises(RuntimeError, match=message):
+        _lib.check(status, "probe")
