@@ -20,7 +20,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import os
 import platform
 import sys
 import time
@@ -44,9 +43,12 @@ def parse_args(argv=None):
     p.add_argument("--check-layers", default="0", help="comma list of layers checked vs the oracle; '' = none")
     p.add_argument("--cpu-baseline-layers", type=int, default=28,
                    help="layers in the CPU baseline sample (0 disables it)")
-    p.add_argument("--cpu-baseline-repeats", type=int, default=2)
+    p.add_argument("--cpu-baseline-repeats", type=int, default=9)
     p.add_argument("--profile", action="store_true",
                    help="run warmup + timed steps only (no check, no CPU baseline), for rocprofv3")
+    p.add_argument("--copy-calibration-mib", type=int, default=0,
+                   help="only run a plain device copy of this many MiB 3 times (the known-size "
+                        "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
     return p.parse_args(argv)
 
 
@@ -73,6 +75,15 @@ def main(argv=None) -> int:
     if torch.version.hip is None or not torch.cuda.is_available():
         raise RuntimeError("bench.py needs a ROCm GPU")
     device = torch.device("cuda", 0)
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n // 2, dtype=torch.int16, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 3}), flush=True)
+        return 0
     backend = create_paged_kv_backend("hip")
 
     wl = workloads.build("decode_step", num_layers=args.layers)
@@ -177,11 +188,15 @@ def main(argv=None) -> int:
     gather_mean = sum(gather_us) / len(gather_us)
     achieved = gather_launch_bytes / (gather_mean * 1e-6) / 1e9
 
+    # HBM bytes per gather launch, from the committed rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE passes (calibrated against a copy of known size); valid only
+    # for this workload, whose algorithmic bytes it was measured against.
     traffic = None
     if TRAFFIC_FILE.is_file():
         try:
             t = json.loads(TRAFFIC_FILE.read_text())
-            if t.get("workload") == "decode_step" and t.get("layers_per_launch") == 1:
+            if (t.get("workload") == "decode_step" and t.get("layers_per_launch") == 1
+                    and t.get("algorithmic_bytes_per_launch") == wl.gather_bytes(layers=1)):
                 traffic = t.get("bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
@@ -234,6 +249,7 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / MI355X_HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": "profiles/gather_varlen_decode_step_traffic.json" if traffic else None,
             "algorithmic_bytes_per_launch": gather_launch_bytes,
         },
         "cpu_baseline": cpu_baseline,

@@ -153,7 +153,8 @@ int nkv_build_gather_plan(const int32_t* block_tables, int64_t table_stride,
 int nkv_gather_varlen_planned(const void* key_cache, const void* value_cache,
                               const void* plan, int64_t capacity,
                               int64_t cache_rows, int64_t out_rows,
-                              int64_t row_elems, int32_t dtype,
+                              int64_t block_size, int64_t row_elems,
+                              int32_t dtype,
                               void* key_out, void* value_out, void* stream);
 
 /*

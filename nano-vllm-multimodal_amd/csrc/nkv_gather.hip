@@ -2,22 +2,34 @@
 //
 // The rows of one cache block are contiguous in memory (block_size rows of
 // row_bytes each), so a sequence's context is a list of contiguous runs, one
-// per logical block.  Every kernel here copies "chunks": chunk_rows
-// consecutive rows that never cross a block (chunk_rows divides block_size),
-// one workgroup per chunk, 256 threads moving 16-byte words with 8 loads in
-// flight per lane per tensor.  This is an HBM-bound streaming copy: loads and
-// stores are non-temporal, there is no LDS staging of payload and no MFMA.
+// per logical block.  The copies are HBM-bound streaming moves: 16-byte
+// words, consecutive lanes on consecutive words, non-temporal loads and
+// stores, no LDS staging of payload and no MFMA.
+//
+// Launch shape (measured on MI355X, decode-step gather of 7.3 GB): many
+// short-lived 128-thread workgroups, each moving ~4 KiB of ONE tensor with
+// a single load in flight per lane (load, store, load, store), reach
+// ~6.4 TB/s; long-lived workgroups streaming 32 KiB with 8 loads in flight
+// per lane stay near 5.3 TB/s, two loads in flight per lane lose ~10%, and
+// a workgroup that moves K and V together (four concurrent streams) loses
+// to K and V in separate workgroups.  The write side is the limit: on this
+// part pure writes top out near 5.6 TB/s while pure non-temporal reads
+// reach 7.2 TB/s.  So the gather launches one workgroup per "sub-chunk" of
+// sub_rows rows (sub_rows * row_bytes <= NKV_GATHER_WG_BYTES), with
+// blockIdx.y selecting K or V; all K workgroups dispatch before the V ones.
 //
 //  * gather_seq_kernel   — the reference op gather(cache, table, L)
 //    (csrc/paged_kv/paged_kv_cuda.cu:61-94,134-164; oracle
-//    nanovllm/layers/paged_kv/pytorch_backend.py:40-50); the chunk's source
-//    block is read straight from the table.
+//    nanovllm/layers/paged_kv/pytorch_backend.py:40-50); each workgroup reads
+//    its source block straight from the table.
 //  * build_plan_kernel   — turns block_tables + cu_seqlens_k of a whole batch
-//    into a flat list of chunks {src_row, dst_row, num_rows, seq}; every
-//    workgroup rescans the per-sequence chunk counts in LDS (wavefront prefix
-//    scan), so the plan needs one launch and no grid-wide sync.
+//    into a flat list of chunks {src_row, dst_row, num_rows, seq} of
+//    chunk_rows rows (a divisor of block_size); every workgroup rescans the
+//    per-sequence chunk counts in LDS (wavefront prefix scan), so the plan
+//    needs one launch and no grid-wide sync.
 //  * gather_planned_kernel — one launch gathers K and V of every sequence of
-//    the batch from a plan, replacing the reference's per-request loop
+//    the batch from a plan (chunk_rows / sub_rows workgroups per entry),
+//    replacing the reference's per-request loop
 //    (nanovllm/layers/attention.py:250-259, 284-292) of one launch per
 //    (request, K or V).
 #include <cstdlib>
@@ -27,10 +39,50 @@
 namespace nkv {
 namespace {
 
-constexpr int kGatherThreads = 256;
-constexpr int kGatherUnroll = 8;
+// Launch-shape knobs (compile-time, for tuning sweeps): workgroup size,
+// words in flight per lane per tensor, whether payload loads / stores carry
+// the non-temporal hint, the plan granularity, the bytes one workgroup
+// moves, and whether K and V go to separate workgroups.
+#ifndef NKV_GATHER_THREADS
+#define NKV_GATHER_THREADS 128
+#endif
+#ifndef NKV_GATHER_UNROLL
+#define NKV_GATHER_UNROLL 1
+#endif
+#ifndef NKV_GATHER_WG_BYTES
+#define NKV_GATHER_WG_BYTES 4096
+#endif
+#ifndef NKV_GATHER_SPLIT_KV
+#define NKV_GATHER_SPLIT_KV 1
+#endif
+#ifndef NKV_GATHER_NT_LOADS
+#define NKV_GATHER_NT_LOADS 1
+#endif
+#ifndef NKV_GATHER_NT_STORES
+#define NKV_GATHER_NT_STORES 1
+#endif
+#ifndef NKV_GATHER_CHUNK_BYTES
+#define NKV_GATHER_CHUNK_BYTES 32768
+#endif
+
+constexpr int kGatherThreads = NKV_GATHER_THREADS;
+constexpr int kGatherUnroll = NKV_GATHER_UNROLL;
 constexpr int kPlanThreads = 1024;
-constexpr int64_t kDefaultChunkBytes = 32768;
+constexpr int64_t kDefaultChunkBytes = NKV_GATHER_CHUNK_BYTES;
+
+template <typename T>
+__device__ __forceinline__ T load_payload(const T* p) {
+  if constexpr (NKV_GATHER_NT_LOADS) return load_stream(p);
+  return *p;
+}
+template <typename T>
+__device__ __forceinline__ void store_payload(T* p, T v) {
+  if constexpr (NKV_GATHER_NT_STORES) {
+    store_stream(p, v);
+  } else {
+    *p = v;
+  }
+}
 
 int64_t chunk_bytes_target() {
   static const int64_t value = [] {
@@ -44,15 +96,26 @@ int64_t chunk_bytes_target() {
   return value;
 }
 
-// Largest divisor of block_size that is <= the target rows per chunk.
-int64_t chunk_rows_for(int64_t block_size, int64_t row_bytes) {
-  int64_t target = chunk_bytes_target() / row_bytes;
+// Largest divisor of `rows` that is <= max(1, target_bytes / row_bytes).
+int64_t divisor_rows(int64_t rows, int64_t row_bytes, int64_t target_bytes) {
+  int64_t target = target_bytes / row_bytes;
   if (target < 1) target = 1;
-  if (target >= block_size) return block_size;
+  if (target >= rows) return rows;
   for (int64_t r = target; r > 1; --r) {
-    if (block_size % r == 0) return r;
+    if (rows % r == 0) return r;
   }
   return 1;
+}
+
+// Plan granularity: a divisor of block_size, ~NKV_GATHER_CHUNK_BYTES.
+int64_t chunk_rows_for(int64_t block_size, int64_t row_bytes) {
+  return divisor_rows(block_size, row_bytes, chunk_bytes_target());
+}
+
+// Rows one workgroup moves: a divisor of `rows` (the plan chunk, or the
+// block for the single-sequence gather), ~NKV_GATHER_WG_BYTES.
+int64_t sub_rows_for(int64_t rows, int64_t row_bytes) {
+  return divisor_rows(rows, row_bytes, NKV_GATHER_WG_BYTES);
 }
 
 // Copies nwords words from s0 to d0 (and s1 to d1 when TWO) with the whole
@@ -76,21 +139,21 @@ __device__ __forceinline__ void copy_chunk(const uint8_t* __restrict__ src0,
     T b[kGatherUnroll];
 #pragma unroll
     for (int u = 0; u < kGatherUnroll; ++u) {
-      a[u] = load_stream(s0 + i + u * kGatherThreads);
-      if constexpr (TWO) b[u] = load_stream(s1 + i + u * kGatherThreads);
+      a[u] = load_payload(s0 + i + u * kGatherThreads);
+      if constexpr (TWO) b[u] = load_payload(s1 + i + u * kGatherThreads);
     }
 #pragma unroll
     for (int u = 0; u < kGatherUnroll; ++u) {
-      store_stream(d0 + i + u * kGatherThreads, a[u]);
-      if constexpr (TWO) store_stream(d1 + i + u * kGatherThreads, b[u]);
+      store_payload(d0 + i + u * kGatherThreads, a[u]);
+      if constexpr (TWO) store_payload(d1 + i + u * kGatherThreads, b[u]);
     }
   }
   for (; i < nwords; i += kGatherThreads) {
-    const T a = load_stream(s0 + i);
+    const T a = load_payload(s0 + i);
     T b{};
-    if constexpr (TWO) b = load_stream(s1 + i);
-    store_stream(d0 + i, a);
-    if constexpr (TWO) store_stream(d1 + i, b);
+    if constexpr (TWO) b = load_payload(s1 + i);
+    store_payload(d0 + i, a);
+    if constexpr (TWO) store_payload(d1 + i, b);
   }
 }
 
@@ -174,28 +237,39 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
   }
 }
 
-// Plan entries are re-checked against the actual cache and output sizes
-// (workgroup-uniform scalar compares), so a plan built for another geometry
-// can never make this kernel read or write out of bounds.
-template <int W, bool TWO>
+// One workgroup per sub-chunk of a plan entry: blockIdx.x = entry *
+// subs_per_entry + sub, blockIdx.y = 0 for K, 1 for V (or one workgroup
+// moving both when SPLIT is false).  Plan entries are re-checked against the
+// actual cache and output sizes (workgroup-uniform scalar compares), so a
+// plan built for another geometry can never make this kernel read or write
+// out of bounds.
+template <int W, bool TWO_IN_ONE>
 __global__ __launch_bounds__(kGatherThreads) void gather_planned_kernel(
     const uint8_t* __restrict__ key_cache,
     const uint8_t* __restrict__ value_cache, const int4* __restrict__ plan,
-    int64_t cache_rows, int64_t out_rows, int64_t row_bytes,
-    uint8_t* __restrict__ key_out, uint8_t* __restrict__ value_out) {
-  const int4 entry = plan[blockIdx.x];
-  if (entry.z <= 0 || entry.y < 0 || static_cast<int64_t>(entry.y) + entry.z > out_rows) {
+    int32_t subs_per_entry, int32_t sub_rows, int64_t cache_rows,
+    int64_t out_rows, int64_t row_bytes, uint8_t* __restrict__ key_out,
+    uint8_t* __restrict__ value_out) {
+  const int32_t e = blockIdx.x / subs_per_entry;
+  const int32_t row_off = (blockIdx.x - e * subs_per_entry) * sub_rows;
+  const int4 entry = plan[e];
+  if (entry.z <= row_off || entry.y < 0 ||
+      static_cast<int64_t>(entry.y) + entry.z > out_rows) {
     return;
   }
-  const int64_t dst = entry.y * row_bytes;
-  const auto nwords = static_cast<int32_t>(entry.z * row_bytes / W);
+  const int32_t nrows = min(sub_rows, entry.z - row_off);
+  const bool second = blockIdx.y != 0;
+  const uint8_t* cache = second ? value_cache : key_cache;
+  uint8_t* out = second ? value_out : key_out;
+  const int64_t dst = (static_cast<int64_t>(entry.y) + row_off) * row_bytes;
+  const auto nwords = static_cast<int32_t>(nrows * row_bytes / W);
   if (entry.x < 0 || static_cast<int64_t>(entry.x) + entry.z > cache_rows) {
-    zero_chunk<W, TWO>(key_out + dst, value_out + dst, nwords);
+    zero_chunk<W, TWO_IN_ONE>(out + dst, value_out + dst, nwords);
     return;
   }
-  const int64_t src = entry.x * row_bytes;
-  copy_chunk<W, TWO>(key_cache + src, key_out + dst, value_cache + src,
-                     value_out + dst, nwords);
+  const int64_t src = (static_cast<int64_t>(entry.x) + row_off) * row_bytes;
+  copy_chunk<W, TWO_IN_ONE>(cache + src, out + dst, value_cache + src,
+                            value_out + dst, nwords);
 }
 
 template <int W>
@@ -212,16 +286,19 @@ int launch_gather_seq(const void* cache, const int32_t* table, int32_t len,
   return nkv_check_launch("nkv_gather");
 }
 
-template <int W, bool TWO>
+template <int W, bool TWO_IN_ONE>
 int launch_planned(const void* key_cache, const void* value_cache,
-                   const void* plan, int64_t capacity, int64_t cache_rows,
-                   int64_t out_rows, int64_t row_bytes, void* key_out,
-                   void* value_out, hipStream_t stream) {
-  gather_planned_kernel<W, TWO><<<dim3(static_cast<unsigned>(capacity)),
-                                  dim3(kGatherThreads), 0, stream>>>(
+                   const void* plan, int64_t capacity, int64_t subs,
+                   int64_t sub_rows, int64_t cache_rows, int64_t out_rows,
+                   int64_t row_bytes, void* key_out, void* value_out,
+                   unsigned grid_y, hipStream_t stream) {
+  gather_planned_kernel<W, TWO_IN_ONE>
+      <<<dim3(static_cast<unsigned>(capacity * subs), grid_y),
+         dim3(kGatherThreads), 0, stream>>>(
       static_cast<const uint8_t*>(key_cache),
       static_cast<const uint8_t*>(value_cache),
-      static_cast<const int4*>(plan), cache_rows, out_rows, row_bytes,
+      static_cast<const int4*>(plan), static_cast<int32_t>(subs),
+      static_cast<int32_t>(sub_rows), cache_rows, out_rows, row_bytes,
       static_cast<uint8_t*>(key_out), static_cast<uint8_t*>(value_out));
   return nkv_check_launch("nkv_gather_varlen_planned");
 }
@@ -293,7 +370,7 @@ extern "C" int nkv_gather(const void* cache, const int32_t* block_table,
     return nkv_fail(NKV_E_INVALID, "nkv_gather: null pointer");
   }
   const int64_t row_bytes = row_elems * element_bytes(dtype);
-  const int64_t rows = chunk_rows_for(block_size, row_bytes);
+  const int64_t rows = sub_rows_for(block_size, row_bytes);
   const int w = common_word_bytes({reinterpret_cast<uint64_t>(cache),
                                    reinterpret_cast<uint64_t>(out),
                                    static_cast<uint64_t>(row_bytes)});
@@ -361,7 +438,8 @@ extern "C" int nkv_gather_varlen_planned(const void* key_cache,
                                          const void* value_cache,
                                          const void* plan, int64_t capacity,
                                          int64_t cache_rows, int64_t out_rows,
-                                         int64_t row_elems, int32_t dtype,
+                                         int64_t block_size, int64_t row_elems,
+                                         int32_t dtype,
                                          void* key_out, void* value_out,
                                          void* stream) {
   using namespace nkv;
@@ -383,19 +461,33 @@ extern "C" int nkv_gather_varlen_planned(const void* key_cache,
                     "value_out must be both set or both NULL)");
   }
   const int64_t row_bytes = row_elems * eb;
+  if (block_size <= 0 || block_size > INT32_MAX) {
+    return nkv_fail(NKV_E_INVALID, "nkv_gather_varlen_planned: block_size must be positive");
+  }
+  const int64_t chunk_rows = chunk_rows_for(block_size, row_bytes);
+  const int64_t sub_rows = sub_rows_for(chunk_rows, row_bytes);
+  const int64_t subs = chunk_rows / sub_rows;
+  if (capacity * subs > INT32_MAX) {
+    return nkv_fail(NKV_E_INVALID, "nkv_gather_varlen_planned: plan too large for one launch");
+  }
   const int w = common_word_bytes(
       {reinterpret_cast<uint64_t>(key_cache), reinterpret_cast<uint64_t>(key_out),
        reinterpret_cast<uint64_t>(two ? value_cache : key_cache),
        reinterpret_cast<uint64_t>(two ? value_out : key_out),
        static_cast<uint64_t>(row_bytes)});
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define NKV_PLANNED(WB)                                                          \
-  return two ? launch_planned<WB, true>(key_cache, value_cache, plan, capacity, \
-                                        cache_rows, out_rows, row_bytes,        \
-                                        key_out, value_out, s)                  \
-             : launch_planned<WB, false>(key_cache, nullptr, plan, capacity,    \
-                                         cache_rows, out_rows, row_bytes,       \
-                                         key_out, nullptr, s)
+  // K and V in separate workgroups (grid y = 2) unless NKV_GATHER_SPLIT_KV=0.
+  const bool together = two && !NKV_GATHER_SPLIT_KV;
+  const unsigned grid_y = (two && NKV_GATHER_SPLIT_KV) ? 2u : 1u;
+#define NKV_PLANNED(WB)                                                        \
+  return together ? launch_planned<WB, true>(key_cache, value_cache, plan,    \
+                                             capacity, subs, sub_rows,        \
+                                             cache_rows, out_rows, row_bytes, \
+                                             key_out, value_out, 1u, s)       \
+                  : launch_planned<WB, false>(key_cache, value_cache, plan,   \
+                                              capacity, subs, sub_rows,       \
+                                              cache_rows, out_rows, row_bytes,\
+                                              key_out, value_out, grid_y, s)
   switch (w) {
     case 16:
       NKV_PLANNED(16);
@@ -442,6 +534,6 @@ extern "C" int nkv_gather_varlen(const void* key_cache, const void* value_cache,
   }
   return nkv_gather_varlen_planned(key_cache, value_cache, workspace, capacity,
                                    num_blocks * block_size, total_rows,
-                                   row_elems, dtype, key_out, value_out,
-                                   stream);
+                                   block_size, row_elems, dtype, key_out,
+                                   value_out, stream);
 }

@@ -8,6 +8,8 @@ loader's message: there is no fallback path.
 from __future__ import annotations
 
 import ctypes
+import os
+from pathlib import Path
 from threading import Lock
 
 from nanokv.build import LIBRARY_PATH
@@ -36,7 +38,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "nkv_gather_varlen_planned": (
         ctypes.c_int,
-        (c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr),
+        (c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr),
     ),
     "nkv_gather_varlen": (
         ctypes.c_int,
@@ -69,7 +71,9 @@ _LIBRARY: ctypes.CDLL | None = None
 
 
 def library_path() -> str:
-    return str(LIBRARY_PATH)
+    """The in-tree build, unless NANOKV_LIBRARY names another build of the
+    same ABI (e.g. one compiled with different launch-shape knobs)."""
+    return os.environ.get("NANOKV_LIBRARY") or str(LIBRARY_PATH)
 
 
 def load_library() -> ctypes.CDLL:
@@ -79,20 +83,21 @@ def load_library() -> ctypes.CDLL:
         return _LIBRARY
     with _LOCK:
         if _LIBRARY is None:
-            if not LIBRARY_PATH.is_file():
+            path = Path(library_path())
+            if not path.is_file():
                 raise RuntimeError(
-                    f"nanokv HIP library not built: {LIBRARY_PATH} is missing "
+                    f"nanokv HIP library not built: {path} is missing "
                     "(run __graft_entry__.build() or python -m nanokv.build)"
                 )
             try:
-                library = ctypes.CDLL(str(LIBRARY_PATH))
+                library = ctypes.CDLL(str(path))
             except OSError as exc:
-                raise RuntimeError(f"failed to load {LIBRARY_PATH}: {exc}") from exc
+                raise RuntimeError(f"failed to load {path}: {exc}") from exc
             for name, (restype, argtypes) in SIGNATURES.items():
                 try:
                     function = getattr(library, name)
                 except AttributeError as exc:
-                    raise RuntimeError(f"{LIBRARY_PATH} does not export {name}") from exc
+                    raise RuntimeError(f"{path} does not export {name}") from exc
                 function.restype = restype
                 function.argtypes = list(argtypes)
             _LIBRARY = library

@@ -50,10 +50,11 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (set ROCM_PATH); cannot build libnanokv.so")
 
 
-def build_command(output: Path) -> list[str]:
+def build_command(output: Path, defines: dict[str, object] | None = None) -> list[str]:
     return [
         hipcc_path(),
         *HIPCC_FLAGS,
+        *(f"-D{key}={value}" for key, value in (defines or {}).items()),
         f"-I{INCLUDE_DIR}",
         *(str(SOURCE_DIR / name) for name in SOURCES),
         "-o",
@@ -61,15 +62,20 @@ def build_command(output: Path) -> list[str]:
     ]
 
 
-def build(*, verbose: bool = False) -> Path:
+def build(*, verbose: bool = False, output: Path | None = None,
+          defines: dict[str, object] | None = None) -> Path:
     """Compile the library (always, even if a build exists) and install it
-    atomically at :data:`LIBRARY_PATH`."""
+    atomically at ``output`` (default :data:`LIBRARY_PATH`).  ``defines``
+    override the kernels' compile-time launch-shape knobs
+    (NKV_GATHER_THREADS, NKV_GATHER_UNROLL, NKV_GATHER_NT_LOADS,
+    NKV_GATHER_NT_STORES, NKV_GATHER_CHUNK_BYTES)."""
+    target = Path(output) if output is not None else LIBRARY_PATH
     missing = [name for name in SOURCES if not (SOURCE_DIR / name).is_file()]
     if missing:
         raise RuntimeError(f"nanokv sources missing: {', '.join(missing)}")
     with tempfile.TemporaryDirectory(prefix="nanokv-build-") as tmp:
         output = Path(tmp) / LIBRARY_PATH.name
-        command = build_command(output)
+        command = build_command(output, defines)
         if verbose:
             print(" ".join(command), flush=True)
         result = subprocess.run(command, capture_output=True, text=True)
@@ -85,10 +91,11 @@ def build(*, verbose: bool = False) -> Path:
             )
         if diagnostics and verbose:
             print(diagnostics, flush=True)
-        staged = LIBRARY_PATH.with_name(LIBRARY_PATH.name + ".tmp")
+        target.parent.mkdir(parents=True, exist_ok=True)
+        staged = target.with_name(target.name + ".tmp")
         shutil.copyfile(output, staged)
-        os.replace(staged, LIBRARY_PATH)
-    return LIBRARY_PATH
+        os.replace(staged, target)
+    return target
 
 
 if __name__ == "__main__":

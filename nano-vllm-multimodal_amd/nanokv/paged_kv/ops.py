@@ -189,6 +189,7 @@ def _gather_planned_impl(key_cache, value_cache, plan, key_out, value_out) -> No
         plan.shape[0],
         key_cache.shape[0] * key_cache.shape[1],
         key_out.shape[0],
+        key_cache.shape[1],
         row_elems,
         dtype_code(key_cache.dtype),
         key_out.data_ptr(),
