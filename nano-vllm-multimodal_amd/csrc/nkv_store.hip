@@ -4,20 +4,28 @@
 // (nanovllm/layers/paged_kv/pytorch_backend.py:26-38): rows whose slot is -1
 // are skipped, every other row t lands in cache row slot_mapping[t]
 // (row = one (block, in-block slot) pair of the [num_blocks, block_size,
-// kv_heads, head_dim] cache).  K and V are moved in the same pass.
+// kv_heads, head_dim] cache).  K and V are moved by the same launch.
 //
-// Mapping: one 64-lane wavefront per group of rows.  A row of row_words
-// words is walked by lanes_per_row = min(64, pow2ceil(row_words)) lanes, so
-// a 2 KiB bf16 row (8 kv heads x 128) is one wavefront issuing 2 K and 2 V
-// 16-byte loads per lane before any store, and a 512 B row (2 x 128) puts two
-// rows in one wavefront.  The work is pure bandwidth (no MFMA, no LDS).
+// Launch shape: the one measured best for paged-KV copies on MI355X (see
+// nkv_gather.hip): short-lived 128-thread workgroups, each moving ~4 KiB of
+// ONE tensor (K rows in blockIdx.y == 0, V rows in blockIdx.y == 1) with
+// one 16-byte word in flight per lane and non-temporal accesses.  A
+// workgroup takes rows_per_wg consecutive tokens (2 rows of 2 KiB, 8 of
+// 512 B); consecutive lanes move consecutive words of a row.  The work is
+// pure bandwidth (no MFMA, no LDS).
 #include "nkv_common.h"
 
 namespace nkv {
 namespace {
 
-constexpr int kStoreThreads = 256;
-constexpr int kStoreMaxBlocks = 16384;
+#ifndef NKV_STORE_THREADS
+#define NKV_STORE_THREADS 128
+#endif
+#ifndef NKV_STORE_WG_BYTES
+#define NKV_STORE_WG_BYTES 4096
+#endif
+
+constexpr int kStoreThreads = NKV_STORE_THREADS;
 
 template <int W>
 __global__ __launch_bounds__(kStoreThreads) void store_rows_kernel(
@@ -25,40 +33,21 @@ __global__ __launch_bounds__(kStoreThreads) void store_rows_kernel(
     uint8_t* __restrict__ key_cache, uint8_t* __restrict__ value_cache,
     const int32_t* __restrict__ slot_mapping, int32_t num_tokens,
     int64_t key_stride, int64_t value_stride, int64_t row_bytes,
-    int32_t row_words, int32_t lpr_shift, int64_t num_slots) {
+    int32_t row_words, int32_t rows_per_wg, int64_t num_slots) {
   using T = typename Word<W>::type;
-  const int32_t lane = threadIdx.x & (kWave - 1);
-  const int32_t lanes_per_row = 1 << lpr_shift;
-  const int32_t rows_per_wave = kWave >> lpr_shift;
-  const int32_t col0 = lane & (lanes_per_row - 1);
-  const int32_t sub = lane >> lpr_shift;
-  const int32_t wave = (blockIdx.x * kStoreThreads + threadIdx.x) / kWave;
-  const int32_t num_waves = (gridDim.x * kStoreThreads) / kWave;
-  for (int32_t t = wave * rows_per_wave + sub; t < num_tokens;
-       t += num_waves * rows_per_wave) {
-    const int32_t slot = slot_mapping[t];
+  const bool second = blockIdx.y != 0;
+  const uint8_t* src = second ? value : key;
+  const int64_t stride = second ? value_stride : key_stride;
+  uint8_t* dst = second ? value_cache : key_cache;
+  const int32_t t0 = blockIdx.x * rows_per_wg;  // < num_tokens by the grid
+  const int32_t nwords = min(rows_per_wg, num_tokens - t0) * row_words;
+  for (int32_t w = threadIdx.x; w < nwords; w += kStoreThreads) {
+    const int32_t r = w / row_words;
+    const int32_t c = w - r * row_words;
+    const int32_t slot = slot_mapping[t0 + r];
     if (slot < 0 || slot >= num_slots) continue;  // -1 padding (and garbage)
-    const T* ks = reinterpret_cast<const T*>(key + t * key_stride);
-    const T* vs = reinterpret_cast<const T*>(value + t * value_stride);
-    T* kd = reinterpret_cast<T*>(key_cache + slot * row_bytes);
-    T* vd = reinterpret_cast<T*>(value_cache + slot * row_bytes);
-    for (int32_t c = col0; c < row_words; c += 2 * lanes_per_row) {
-      const int32_t c1 = c + lanes_per_row;
-      const bool two = c1 < row_words;
-      const T k0 = ks[c];
-      const T v0 = vs[c];
-      T k1{}, v1{};
-      if (two) {
-        k1 = ks[c1];
-        v1 = vs[c1];
-      }
-      kd[c] = k0;
-      vd[c] = v0;
-      if (two) {
-        kd[c1] = k1;
-        vd[c1] = v1;
-      }
-    }
+    const T v = load_stream(reinterpret_cast<const T*>(src + (t0 + r) * stride) + c);
+    store_stream(reinterpret_cast<T*>(dst + slot * row_bytes) + c, v);
   }
 }
 
@@ -68,19 +57,16 @@ int launch_store(const void* key, const void* value, void* key_cache,
                  int64_t ks, int64_t vs, int64_t row_bytes, int64_t num_slots,
                  hipStream_t stream) {
   const int64_t row_words = row_bytes / W;
-  int lpr_shift = 0;
-  while ((int64_t{1} << lpr_shift) < row_words && lpr_shift < 6) ++lpr_shift;
-  const int64_t rows_per_wave = kWave >> lpr_shift;
-  const int64_t waves = (num_tokens + rows_per_wave - 1) / rows_per_wave;
-  const int64_t waves_per_block = kStoreThreads / kWave;
-  int64_t blocks = (waves + waves_per_block - 1) / waves_per_block;
-  if (blocks > kStoreMaxBlocks) blocks = kStoreMaxBlocks;
-  store_rows_kernel<W><<<dim3(static_cast<unsigned>(blocks)),
+  int64_t rows_per_wg = NKV_STORE_WG_BYTES / row_bytes;
+  if (rows_per_wg < 1) rows_per_wg = 1;
+  if (rows_per_wg * row_words > INT32_MAX) rows_per_wg = 1;
+  const int64_t blocks = (num_tokens + rows_per_wg - 1) / rows_per_wg;
+  store_rows_kernel<W><<<dim3(static_cast<unsigned>(blocks), 2),
                          dim3(kStoreThreads), 0, stream>>>(
       static_cast<const uint8_t*>(key), static_cast<const uint8_t*>(value),
       static_cast<uint8_t*>(key_cache), static_cast<uint8_t*>(value_cache),
       slots, num_tokens, ks, vs, row_bytes, static_cast<int32_t>(row_words),
-      lpr_shift, num_slots);
+      static_cast<int32_t>(rows_per_wg), num_slots);
   return nkv_check_launch("nkv_store");
 }
 
