@@ -177,11 +177,17 @@ int nkv_gather_varlen(const void* key_cache, const void* value_cache,
  * Outputs (all int32, device):
  *   slot_mapping[i]  = last_block*block_size + last_block_num_tokens - 1
  *                      (-1 when the block list is empty)
- *   context_lens[i]  = num_tokens[i]
- *   block_tables     [num_seqs, table_width], -1 padded; table_width must
- *                    be >= the longest block list
- *   cu_seqlens_k     [num_seqs+1], exclusive prefix sum of num_tokens
+ *   context_lens[i]  = num_tokens[i]                          (may be NULL)
+ *   block_tables     rows of table_stride entries: columns [0, table_width)
+ *                    of rows [0, num_seqs) get the block list, -1 padded;
+ *                    table_width must be >= the longest block list, and
+ *                    columns >= table_width keep their contents (may be NULL)
+ *   cu_seqlens_k     [padded_seqs+1], exclusive prefix sum of num_tokens
  *                    (may be NULL)
+ * Rows [num_seqs, padded_seqs) are graph-bucket padding: slot -1, context
+ * length 0, cu_seqlens_k flat, block-table rows untouched.  Writing into
+ * fixed buffers this way reproduces the decode graph's replay fill
+ * (model_runner.py:993-1011) without the -1/0 fills and D2D copies.
  *
  * Replaces: ModelRunner.prepare_decode's host loop and copies
  *   (nanovllm/engine/model_runner.py:892-938), the slot formula with
@@ -191,11 +197,11 @@ int nkv_gather_varlen(const void* key_cache, const void* value_cache,
 #define NKV_MAX_PACK_SEQS 4096
 int nkv_pack_decode(const int32_t* num_tokens, const int32_t* block_offsets,
                     const int32_t* block_ids, int64_t num_block_ids,
-                    int64_t num_seqs,
+                    int64_t num_seqs, int64_t padded_seqs,
                     int64_t block_size, int64_t table_width,
-                    int32_t* slot_mapping, int32_t* context_lens,
-                    int32_t* block_tables, int32_t* cu_seqlens_k,
-                    void* stream);
+                    int64_t table_stride, int32_t* slot_mapping,
+                    int32_t* context_lens, int32_t* block_tables,
+                    int32_t* cu_seqlens_k, void* stream);
 
 /*
  * Prefill / chunked-prefill metadata packing on the device.  Per sequence:

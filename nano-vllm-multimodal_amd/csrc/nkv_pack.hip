@@ -27,23 +27,29 @@ __device__ __forceinline__ int32_t csr_read(const int32_t* __restrict__ ids,
   return (k >= 0 && k < nnz) ? ids[k] : -1;
 }
 
-// One wavefront writes block_tables[i, 0:width) for sequence i.
+// One wavefront writes block_tables[i, 0:width) for sequence i (rows are
+// `stride` entries apart; columns >= width are left as they are).
 __device__ __forceinline__ void write_table_row(
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ ids,
-    int64_t nnz, int32_t i, int32_t width, int32_t* __restrict__ tables) {
+    int64_t nnz, int32_t i, int32_t width, int64_t stride,
+    int32_t* __restrict__ tables) {
   const int32_t lane = threadIdx.x & (kWave - 1);
   const int32_t begin = offsets[i];
   const int32_t count = offsets[i + 1] - begin;
-  int32_t* row = tables + static_cast<int64_t>(i) * width;
+  int32_t* row = tables + static_cast<int64_t>(i) * stride;
   for (int32_t j = lane; j < width; j += kWave) {
     row[j] = j < count ? csr_read(ids, nnz, static_cast<int64_t>(begin) + j) : -1;
   }
 }
 
+// Sequences [num_seqs, padded_seqs) are graph-bucket padding: slot -1,
+// context length 0, cu_seqlens_k flat at the total, block-table rows left
+// as they are (the fill of model_runner.py:998-1011).
 __global__ __launch_bounds__(kPackThreads) void pack_decode_kernel(
     const int32_t* __restrict__ num_tokens, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ ids, int64_t nnz, int32_t num_seqs,
-    int32_t block_size, int32_t width, int32_t* __restrict__ slot_mapping,
+    int32_t padded_seqs, int32_t block_size, int32_t width,
+    int64_t table_stride, int32_t* __restrict__ slot_mapping,
     int32_t* __restrict__ context_lens, int32_t* __restrict__ tables,
     int32_t* __restrict__ cu_seqlens_k) {
   extern __shared__ int32_t s_mem[];
@@ -53,15 +59,22 @@ __global__ __launch_bounds__(kPackThreads) void pack_decode_kernel(
     lds_exclusive_scan<kPackThreads>(
         num_seqs, [&](int32_t i) { return max(num_tokens[i], 0); }, s_cu,
         s_tmp);
-    for (int32_t i = threadIdx.x; i <= num_seqs; i += kPackThreads) {
-      cu_seqlens_k[i] = s_cu[i];
+    for (int32_t i = threadIdx.x; i <= padded_seqs; i += kPackThreads) {
+      cu_seqlens_k[i] = s_cu[min(i, num_seqs)];
     }
   }
   const int32_t lane = threadIdx.x & (kWave - 1);
   const int32_t num_waves = gridDim.x * kPackWaves;
-  for (int32_t i = blockIdx.x * kPackWaves + threadIdx.x / kWave; i < num_seqs;
+  for (int32_t i = blockIdx.x * kPackWaves + threadIdx.x / kWave; i < padded_seqs;
        i += num_waves) {
-    if (tables != nullptr) write_table_row(offsets, ids, nnz, i, width, tables);
+    if (i >= num_seqs) {
+      if (lane == 0) {
+        slot_mapping[i] = -1;
+        if (context_lens != nullptr) context_lens[i] = 0;
+      }
+      continue;
+    }
+    if (tables != nullptr) write_table_row(offsets, ids, nnz, i, width, table_stride, tables);
     if (lane == 0) {
       const int32_t n = num_tokens[i];
       const int32_t end = offsets[i + 1];
@@ -164,7 +177,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_prefill_kernel(
     const int32_t num_waves = gridDim.x * kPackWaves;
     for (int32_t i = blockIdx.x * kPackWaves + threadIdx.x / kWave;
          i < num_seqs; i += num_waves) {
-      write_table_row(offsets, ids, nnz, i, width, tables);
+      write_table_row(offsets, ids, nnz, i, width, width, tables);
     }
   }
 
@@ -220,8 +233,9 @@ unsigned pack_grid(int64_t num_seqs, int64_t items) {
 extern "C" int nkv_pack_decode(const int32_t* num_tokens,
                                const int32_t* block_offsets,
                                const int32_t* block_ids, int64_t num_block_ids,
-                               int64_t num_seqs, int64_t block_size,
-                               int64_t table_width, int32_t* slot_mapping,
+                               int64_t num_seqs, int64_t padded_seqs,
+                               int64_t block_size, int64_t table_width,
+                               int64_t table_stride, int32_t* slot_mapping,
                                int32_t* context_lens, int32_t* block_tables,
                                int32_t* cu_seqlens_k, void* stream) {
   using namespace nkv;
@@ -229,22 +243,31 @@ extern "C" int nkv_pack_decode(const int32_t* num_tokens,
                                block_size, table_width)) {
     return rc;
   }
-  // An empty batch still launches when cu_seqlens_k must get its single 0
-  // (a kernel rather than a memset, so the call stays graph-capturable).
-  if (num_seqs == 0 && cu_seqlens_k == nullptr) return NKV_OK;
-  if (num_seqs > 0 && (!num_tokens || !block_offsets || !slot_mapping ||
-                       (num_block_ids > 0 && !block_ids))) {
+  if (padded_seqs < num_seqs || padded_seqs > NKV_MAX_PACK_SEQS) {
+    return nkv_fail(NKV_E_INVALID,
+                    "nkv_pack_decode: padded_seqs=%lld must be in [num_seqs, %d]",
+                    static_cast<long long>(padded_seqs), NKV_MAX_PACK_SEQS);
+  }
+  if (table_stride < table_width) {
+    return nkv_fail(NKV_E_INVALID, "nkv_pack_decode: table_stride < table_width");
+  }
+  // An empty batch still launches when cu_seqlens_k or padding must be
+  // written (a kernel rather than a memset, so the call stays
+  // graph-capturable).
+  if (padded_seqs == 0 && cu_seqlens_k == nullptr) return NKV_OK;
+  if ((padded_seqs > 0 && !slot_mapping) ||
+      (num_seqs > 0 && (!num_tokens || !block_offsets || (num_block_ids > 0 && !block_ids)))) {
     return nkv_fail(NKV_E_INVALID, "nkv_pack_decode: null pointer");
   }
   const size_t lds = cu_seqlens_k != nullptr
                          ? (static_cast<size_t>(num_seqs) + 1 + kPackWaves + 1) * sizeof(int32_t)
                          : 0;
-  pack_decode_kernel<<<dim3(pack_grid(num_seqs, 0)), dim3(kPackThreads), lds,
+  pack_decode_kernel<<<dim3(pack_grid(padded_seqs, 0)), dim3(kPackThreads), lds,
                        static_cast<hipStream_t>(stream)>>>(
       num_tokens, block_offsets, block_ids, num_block_ids,
-      static_cast<int32_t>(num_seqs), static_cast<int32_t>(block_size),
-      static_cast<int32_t>(table_width), slot_mapping, context_lens,
-      block_tables, cu_seqlens_k);
+      static_cast<int32_t>(num_seqs), static_cast<int32_t>(padded_seqs),
+      static_cast<int32_t>(block_size), static_cast<int32_t>(table_width),
+      table_stride, slot_mapping, context_lens, block_tables, cu_seqlens_k);
   return nkv_check_launch("nkv_pack_decode");
 }
 

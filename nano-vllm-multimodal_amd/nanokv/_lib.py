@@ -49,7 +49,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "nkv_pack_decode": (
         ctypes.c_int,
-        (c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr),
+        (c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr),
     ),
     "nkv_pack_prefill": (
         ctypes.c_int,

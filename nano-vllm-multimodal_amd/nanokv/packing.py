@@ -131,6 +131,42 @@ class SequenceBatch:
         )
 
 
+@dataclass
+class DecodeGraphBuffers:
+    """Fixed-address decode metadata for a captured decode graph: the
+    buffers of ModelRunner.capture_cudagraph (model_runner.py:1093-1106,
+    zero-initialised like them) plus cu_seqlens_k for a varlen gather.
+    A graph captured for batch bucket ``bs`` reads the first ``bs`` rows."""
+
+    slot_mapping: torch.Tensor   # [max_num_seqs] int32
+    context_lens: torch.Tensor   # [max_num_seqs] int32
+    block_tables: torch.Tensor   # [max_num_seqs, max_blocks] int32
+    cu_seqlens_k: torch.Tensor   # [max_num_seqs + 1] int32
+
+    @classmethod
+    def allocate(cls, device: torch.device | str, max_num_seqs: int, max_blocks: int) -> "DecodeGraphBuffers":
+        if max_num_seqs <= 0 or max_blocks <= 0:
+            raise ValueError("max_num_seqs and max_blocks must be positive")
+        if max_num_seqs > _lib.NKV_MAX_PACK_SEQS:
+            raise ValueError(f"at most {_lib.NKV_MAX_PACK_SEQS} sequences per decode graph")
+        device = torch.device(device)
+        zeros = lambda *shape: torch.zeros(shape, dtype=torch.int32, device=device)  # noqa: E731
+        return cls(zeros(max_num_seqs), zeros(max_num_seqs), zeros(max_num_seqs, max_blocks),
+                   zeros(max_num_seqs + 1))
+
+    @property
+    def max_num_seqs(self) -> int:
+        return int(self.slot_mapping.numel())
+
+    @property
+    def max_blocks(self) -> int:
+        return int(self.block_tables.shape[1])
+
+    @property
+    def device(self) -> torch.device:
+        return self.slot_mapping.device
+
+
 class DevicePacker:
     """Launches the packing kernels for one device and block size.
 
@@ -145,6 +181,8 @@ class DevicePacker:
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("DevicePacker requires a ROCm (cuda) device")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         if block_size <= 0:
             raise ValueError("block_size must be positive")
         self.block_size = int(block_size)
@@ -216,7 +254,7 @@ class DevicePacker:
         tables = out[3 * b + 1 :].view(b, width)
         status = _lib.load_library().nkv_pack_decode(
             d_tokens.data_ptr(), d_offsets.data_ptr(), d_ids.data_ptr() if d_ids.numel() else None,
-            d_ids.numel(), b, self.block_size, width, slots.data_ptr(),
+            d_ids.numel(), b, b, self.block_size, width, width, slots.data_ptr(),
             context_lens.data_ptr(), tables.data_ptr() if tables.numel() else None,
             cu_seqlens_k.data_ptr(), self._stream(),
         )
@@ -230,6 +268,55 @@ class DevicePacker:
             context_lens=context_lens,
             block_tables=tables,
             total_context_tokens=total,
+        )
+
+    def pack_decode_into(
+        self,
+        batch: SequenceBatch,
+        buffers: "DecodeGraphBuffers",
+        *,
+        padded_seqs: int | None = None,
+    ) -> Context:
+        """Decode packing straight into the fixed-address buffers a captured
+        decode graph reads.  Equals the reference's replay fill
+        (model_runner.py:993-1011): slot_mapping[bs:padded] = -1,
+        context_lens[bs:padded] = 0, block_tables[:bs, :w] = the -1 padded
+        tables with w = the longest block list of the batch, while columns
+        >= w and rows >= bs keep their contents.  ``padded`` defaults to the
+        buffers' capacity (the reference fills the whole max_bs buffers).
+        One kernel, no fills or device-to-device copies, capturable."""
+        self._check_num_seqs(batch)
+        b = batch.num_seqs
+        padded = buffers.max_num_seqs if padded_seqs is None else int(padded_seqs)
+        if not b <= padded <= buffers.max_num_seqs:
+            raise ValueError("padded_seqs must be in [num_seqs, buffers.max_num_seqs]")
+        if b and bool((batch.block_counts < 1).any()):
+            raise ValueError("every decoding sequence needs a non-empty block_table")
+        if b and bool((batch.num_tokens < 1).any()):
+            raise ValueError("every decoding sequence needs at least one token")
+        width = self._width(batch, None)
+        if width > buffers.max_blocks:
+            raise ValueError("a block list is longer than the graph buffers' max_blocks")
+        if buffers.device != self.device:
+            raise ValueError("graph buffers live on another device")
+        d_tokens, d_offsets, d_ids = self._upload(
+            [batch.num_tokens, batch.block_offsets, batch.block_ids]
+        )
+        status = _lib.load_library().nkv_pack_decode(
+            d_tokens.data_ptr(), d_offsets.data_ptr(), d_ids.data_ptr() if d_ids.numel() else None,
+            d_ids.numel(), b, padded, self.block_size, width, buffers.max_blocks,
+            buffers.slot_mapping.data_ptr(), buffers.context_lens.data_ptr(),
+            buffers.block_tables.data_ptr(), buffers.cu_seqlens_k.data_ptr(), self._stream(),
+        )
+        _lib.check(status, "nkv_pack_decode")
+        return Context(
+            is_prefill=False,
+            cu_seqlens_k=buffers.cu_seqlens_k[: b + 1],
+            max_seqlen_k=int(batch.num_tokens.max()) if b else 0,
+            slot_mapping=buffers.slot_mapping[:b],
+            context_lens=buffers.context_lens[:b],
+            block_tables=buffers.block_tables[:b],
+            total_context_tokens=int(batch.num_tokens.astype(np.int64).sum()),
         )
 
     # ------------------------------------------------------------ prefill

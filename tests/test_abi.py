@@ -67,8 +67,10 @@ def test_version_and_plan_geometry():
     (lambda l: l.nkv_build_gather_plan(None, 4, None, 9000, 10, 4, 8, 3, 1, None, 16, None), "num_seqs"),
     (lambda l: l.nkv_gather_varlen_planned(None, None, None, 4, 8, 8, 4, 8, 1, None, None, None), "null"),
     (lambda l: l.nkv_gather_varlen(None, None, None, 1, None, 2, 100, 16, 8, 4, 1, None, None, None, 16, None), "workspace"),
-    (lambda l: l.nkv_pack_decode(None, None, None, 0, 5000, 16, 4, None, None, None, None, None), "num_seqs"),
-    (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 16, 4, None, None, None, None, None), "null"),
+    (lambda l: l.nkv_pack_decode(None, None, None, 0, 5000, 5000, 16, 4, 4, None, None, None, None, None), "num_seqs"),
+    (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 3, 16, 4, 4, None, None, None, None, None), "null"),
+    (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 2, 16, 4, 4, None, None, None, None, None), "padded_seqs"),
+    (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 3, 16, 4, 2, None, None, None, None, None), "table_stride"),
     (lambda l: l.nkv_pack_prefill(None, None, None, None, None, 0, 3, 0, 4, 8, None, None, None, None, None, None, None, None), "block_size"),
 ])
 def test_contract_violations_fail_before_launch(call, message):
