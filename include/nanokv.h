@@ -233,6 +233,33 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
                      int32_t* query_start_lens, int32_t* max_seqlens,
                      void* stream);
 
+/*
+ * Host-to-device transfer lane: a non-blocking transfer stream (default
+ * priority) and recycled events owned by the library.
+ *   nkv_transfer_h2d   copies `bytes` from pinned host `src` to device `dst`
+ *                      on the lane, ordered after all work already enqueued
+ *                      on `compute_stream`, and makes `compute_stream` wait
+ *                      for the copy; returns an increasing ticket.  The host
+ *                      buffer must stay valid until the ticket completes.
+ *   nkv_transfer_poll  in_flight = copies not yet complete; completed_upto =
+ *                      highest completed ticket (copies complete in order).
+ *   nkv_transfer_synchronize waits for every copy; destroy synchronizes too.
+ *
+ * Replaces: the transfer stream, reuse/transfer events and pending-copy
+ *   bookkeeping of PagedKVCache::copy_slots_async
+ *   (csrc/paged_kv/paged_kv.cpp:67-72, 101-168); the reference's grown slot
+ *   buffer and host-tensor retention live with the caller (the Python
+ *   owner nanokv.paged_kv.owner.HIPPagedKVCache).
+ */
+typedef struct nkv_transfer nkv_transfer;
+int nkv_transfer_create(int32_t device, nkv_transfer** out);
+int nkv_transfer_destroy(nkv_transfer* lane);
+int nkv_transfer_h2d(nkv_transfer* lane, void* dst, const void* src,
+                     int64_t bytes, void* compute_stream, int64_t* ticket);
+int nkv_transfer_poll(nkv_transfer* lane, int64_t* in_flight,
+                      int64_t* completed_upto);
+int nkv_transfer_synchronize(nkv_transfer* lane);
+
 #ifdef __cplusplus
 }
 #endif

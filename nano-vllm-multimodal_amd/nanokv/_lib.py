@@ -17,6 +17,8 @@ from nanokv.build import LIBRARY_PATH
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
 c_ptr = ctypes.c_void_p
+c_ptr_out = ctypes.POINTER(ctypes.c_void_p)
+c_i64_out = ctypes.POINTER(ctypes.c_int64)
 
 # name -> (restype, argtypes); mirrors include/nanokv.h.
 SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
@@ -58,6 +60,11 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
             c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
         ),
     ),
+    "nkv_transfer_create": (ctypes.c_int, (c_i32, c_ptr_out)),
+    "nkv_transfer_destroy": (ctypes.c_int, (c_ptr,)),
+    "nkv_transfer_h2d": (ctypes.c_int, (c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64_out)),
+    "nkv_transfer_poll": (ctypes.c_int, (c_ptr, c_i64_out, c_i64_out)),
+    "nkv_transfer_synchronize": (ctypes.c_int, (c_ptr,)),
 }
 
 NKV_DTYPE_FLOAT16 = 0

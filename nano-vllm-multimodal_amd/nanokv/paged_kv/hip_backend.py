@@ -68,7 +68,8 @@ class HIPPagedKVBackend:
         device: torch.device | str,
     ) -> PagedKVAllocation:
         """One device tensor for the whole [2, layers, blocks, block, heads,
-        dim] cache (model_runner.py:657-674); per-layer views of it are
+        dim] cache (model_runner.py:657-674), owned by a native
+        HIPPagedKVCache (cuda_backend.py:44-65); per-layer views of it are
         contiguous, which the kernels require."""
         resolved = torch.device(device)
         if resolved.type != "cuda":
@@ -78,7 +79,18 @@ class HIPPagedKVBackend:
         if any(int(size) <= 0 for size in shape) or not shape:
             raise ValueError("HIP Paged KV allocation dimensions must be positive")
         self._load()
-        return PagedKVAllocation(torch.empty(tuple(int(s) for s in shape), dtype=dtype, device=resolved))
+        from nanokv.paged_kv.owner import HIPPagedKVCache
+
+        index = torch.cuda.current_device() if resolved.index is None else resolved.index
+        owner = HIPPagedKVCache(list(shape), dtype, index)
+        return PagedKVAllocation(owner.tensor(), owner)
+
+    def copy_slots_async(self, allocation: PagedKVAllocation, host_slots: torch.Tensor) -> torch.Tensor:
+        """cuda_backend.py:67-74: pinned host slot mapping -> device through
+        the owner's transfer lane."""
+        if allocation.owner is None:
+            raise ValueError("HIP Paged KV allocation has no native owner")
+        return allocation.owner.copy_slots_async(host_slots)
 
     def store(
         self,

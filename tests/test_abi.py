@@ -18,7 +18,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "nanokv.h"
 
 def declared_functions() -> set[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return set(re.findall(r"\b(nkv_[a-z_]+)\s*\(", text))
+    return set(re.findall(r"\b(nkv_[a-z0-9_]+)\s*\(", text))
 
 
 def test_header_and_binding_agree():
@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(library, name), name
     nm = subprocess.run(["nm", "-D", "--defined-only", str(LIBRARY_PATH)], capture_output=True, text=True)
-    exported = set(re.findall(r"\bT (nkv_[a-z_]+)\b", nm.stdout))
+    exported = set(re.findall(r"\bT (nkv_[a-z0-9_]+)\b", nm.stdout))
     assert declared <= exported, declared - exported
 
 
