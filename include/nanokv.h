@@ -234,6 +234,50 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
                      void* stream);
 
 /*
+ * Paged-attention decode: one query token per sequence attends over its
+ * whole context (context_len = cu_seqlens_k[i+1] - cu_seqlens_k[i]) read
+ * straight from the paged caches, with no gather.
+ *   out[i, h, :] = softmax(scale * q[i, h] . K_i[:, h / G]^T) V_i[:, h / G]
+ * for query head h, G = num_q_heads / num_kv_heads (kv head h / G), in fp32
+ * with a bf16 result.  An empty context yields zeros.  bf16 only,
+ * head_dim 128, num_kv_heads in {1,2,4,8}, at most 16 query heads.
+ *
+ * Replaces: the decode call flash_attn_with_kvcache(q, k_cache, v_cache,
+ *   cache_seqlens=context_lens, block_table=block_tables, softmax_scale,
+ *   causal=True) of Attention.forward (nanovllm/layers/attention.py:
+ *   122-130); numerically the decode branch of SDPAAttention
+ *   (attention.py:284-300: per-request gather, then SDPA with GQA).
+ *
+ * nkv_build_attention_plan writes one int4 entry per (sequence, cache
+ *   block) into `plan` (capacity >= nkv_attention_plan_capacity(total
+ *   context tokens, num_seqs, block_size)) and each sequence's first entry
+ *   into first_part [num_seqs+1]; one plan serves every layer of a step.
+ * nkv_paged_attention_decode runs the split-K partial kernel and the
+ *   merge; workspace holds nkv_attention_workspace_bytes(capacity,
+ *   num_q_heads, head_dim) bytes (16-byte aligned).  q is [num_seqs,
+ *   num_q_heads, head_dim] with row stride q_seq_stride elements; out is
+ *   [num_seqs, num_q_heads, head_dim] with row stride out_seq_stride.
+ */
+int64_t nkv_attention_plan_capacity(int64_t total_tokens, int64_t num_seqs,
+                                    int64_t block_size);
+int64_t nkv_attention_workspace_bytes(int64_t capacity, int64_t num_q_heads,
+                                      int64_t head_dim);
+int nkv_build_attention_plan(const int32_t* block_tables, int64_t table_stride,
+                             const int32_t* cu_seqlens_k, int64_t num_seqs,
+                             int64_t block_size, int64_t num_blocks, void* plan,
+                             int64_t capacity, int32_t* first_part,
+                             void* stream);
+int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
+                               const void* key_cache, const void* value_cache,
+                               const void* plan, int64_t capacity,
+                               const int32_t* first_part, int64_t num_seqs,
+                               int64_t num_kv_heads, int64_t num_q_heads,
+                               int64_t head_dim, int64_t block_size,
+                               int64_t num_blocks, float scale, int32_t dtype,
+                               void* workspace, int64_t workspace_bytes,
+                               void* out, int64_t out_seq_stride, void* stream);
+
+/*
  * Host-to-device transfer lane: a non-blocking transfer stream (default
  * priority) and recycled events owned by the library.
  *   nkv_transfer_h2d   copies `bytes` from pinned host `src` to device `dst`

@@ -156,6 +156,18 @@ __device__ __forceinline__ int32_t owner_of(const int32_t* s, int32_t n,
 // (defined in nkv_api.hip).
 int element_bytes(int32_t dtype);
 
+// Launches the block-table plan builder (defined in nkv_gather.hip): one
+// int4 entry {src_row (-1 if the block id is invalid), dst_row, rows, seq}
+// per chunk of chunk_rows rows (a divisor of block_size) of every sequence
+// in cu_seqlens; first_chunk (optional, [num_seqs+1]) gets each sequence's
+// first entry index.  Callers validate the arguments.
+int launch_block_plan(const int32_t* tables, int64_t table_stride,
+                      const int32_t* cu_seqlens, int64_t num_seqs,
+                      int64_t out_rows, int64_t block_size, int64_t chunk_rows,
+                      int64_t num_blocks, int32_t* plan, int64_t capacity,
+                      int32_t* first_chunk, hipStream_t stream,
+                      const char* what);
+
 }  // namespace nkv
 
 // Error reporting shared by all translation units (defined in nkv_api.hip).

@@ -192,11 +192,14 @@ __global__ __launch_bounds__(kGatherThreads) void gather_seq_kernel(
 
 // Plan entry layout: x = source row (block*block_size + offset, -1 when the
 // block id is invalid), y = destination row, z = rows, w = sequence index.
+// first_chunk (optional, [num_seqs + 1]) receives the index of every
+// sequence's first entry, i.e. the exclusive scan of the chunk counts.
 __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     const int32_t* __restrict__ tables, int64_t table_stride,
     const int32_t* __restrict__ cu_seqlens, int32_t num_seqs,
     int32_t block_size, int32_t chunk_rows, int64_t num_blocks,
-    int64_t out_rows, int4* __restrict__ plan, int64_t capacity) {
+    int64_t out_rows, int4* __restrict__ plan, int64_t capacity,
+    int32_t* __restrict__ first_chunk) {
   extern __shared__ int32_t s_mem[];
   int32_t* s_first = s_mem;                 // [num_seqs + 1]
   int32_t* s_tmp = s_mem + num_seqs + 1;    // [kPlanThreads / 64 + 1]
@@ -207,6 +210,9 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
         return len > 0 ? (len + chunk_rows - 1) / chunk_rows : 0;
       },
       s_first, s_tmp);
+  if (first_chunk != nullptr && blockIdx.x == 0) {
+    for (int32_t i = threadIdx.x; i <= num_seqs; i += kPlanThreads) first_chunk[i] = s_first[i];
+  }
   const int64_t total = s_first[num_seqs];
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x;
@@ -324,6 +330,28 @@ int check_geometry(const char* what, int64_t block_size, int64_t row_elems,
 }
 
 }  // namespace
+
+// Shared by the gather plan and the decode-attention partition plan
+// (chunk_rows = block_size); arguments are validated by the callers.
+int launch_block_plan(const int32_t* tables, int64_t table_stride,
+                      const int32_t* cu_seqlens, int64_t num_seqs,
+                      int64_t out_rows, int64_t block_size, int64_t chunk_rows,
+                      int64_t num_blocks, int32_t* plan, int64_t capacity,
+                      int32_t* first_chunk, hipStream_t stream,
+                      const char* what) {
+  int64_t blocks = (capacity + kPlanThreads - 1) / kPlanThreads;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 1024) blocks = 1024;
+  const size_t lds = (static_cast<size_t>(num_seqs) + 1 + kPlanThreads / kWave + 1) *
+                     sizeof(int32_t);
+  build_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPlanThreads),
+                      lds, stream>>>(
+      tables, table_stride, cu_seqlens, static_cast<int32_t>(num_seqs),
+      static_cast<int32_t>(block_size), static_cast<int32_t>(chunk_rows), num_blocks,
+      out_rows, reinterpret_cast<int4*>(plan), capacity, first_chunk);
+  return nkv_check_launch(what);
+}
+
 }  // namespace nkv
 
 extern "C" int64_t nkv_gather_plan_rows(int64_t block_size, int64_t row_elems,
@@ -422,16 +450,11 @@ extern "C" int nkv_build_gather_plan(const int32_t* block_tables,
   }
   const int64_t row_bytes = row_elems * element_bytes(dtype);
   const int64_t rows = chunk_rows_for(block_size, row_bytes);
-  int64_t blocks = (capacity + kPlanThreads - 1) / kPlanThreads;
-  if (blocks > 1024) blocks = 1024;
-  const size_t lds = (static_cast<size_t>(num_seqs) + 1 + kPlanThreads / kWave + 1) *
-                     sizeof(int32_t);
-  build_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPlanThreads),
-                      lds, static_cast<hipStream_t>(stream)>>>(
-      block_tables, table_stride, cu_seqlens_k, static_cast<int32_t>(num_seqs),
-      static_cast<int32_t>(block_size), static_cast<int32_t>(rows), num_blocks,
-      out_rows, static_cast<int4*>(plan), capacity);
-  return nkv_check_launch("nkv_build_gather_plan");
+  return launch_block_plan(block_tables, table_stride, cu_seqlens_k, num_seqs,
+                           out_rows, block_size, rows, num_blocks,
+                           static_cast<int32_t*>(plan), capacity, nullptr,
+                           static_cast<hipStream_t>(stream),
+                           "nkv_build_gather_plan");
 }
 
 extern "C" int nkv_gather_varlen_planned(const void* key_cache,

@@ -18,7 +18,14 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 SOURCE_DIR = PACKAGE_DIR.parent / "csrc"
 INCLUDE_DIR = PACKAGE_DIR.parents[1] / "include"
 LIBRARY_PATH = PACKAGE_DIR / "libnanokv.so"
-SOURCES = ("nkv_api.hip", "nkv_store.hip", "nkv_gather.hip", "nkv_pack.hip", "nkv_transfer.hip")
+SOURCES = (
+    "nkv_api.hip",
+    "nkv_store.hip",
+    "nkv_gather.hip",
+    "nkv_pack.hip",
+    "nkv_transfer.hip",
+    "nkv_attention.hip",
+)
 OFFLOAD_ARCH = "gfx950"
 HIPCC_FLAGS = (
     f"--offload-arch={OFFLOAD_ARCH}",

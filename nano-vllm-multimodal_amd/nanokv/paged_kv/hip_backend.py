@@ -174,6 +174,57 @@ class HIPPagedKVBackend:
         )
 
 
+    def build_attention_plan(
+        self,
+        cache: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_k: torch.Tensor,
+        total_tokens: int,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """(plan, first_part) for :meth:`paged_attention_decode`: one entry
+        per (sequence, cache block); valid for every layer of the step."""
+        self._load()
+        num_blocks, block_size = cache.shape[:2]
+        return torch.ops.nanovllm_paged_kv.build_attention_plan(
+            block_tables, cu_seqlens_k, total_tokens, num_blocks, block_size
+        )
+
+    def paged_attention_decode(
+        self,
+        q: torch.Tensor,
+        key_cache: torch.Tensor,
+        value_cache: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_k: torch.Tensor,
+        total_tokens: int,
+        softmax_scale: float,
+        *,
+        plan: tuple[torch.Tensor, torch.Tensor] | None = None,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Decode attention read straight from the paged caches: for each
+        sequence i (context length cu_seqlens_k[i+1] - cu_seqlens_k[i]) and
+        query head h, softmax(scale * q[i,h] K_i^T) V_i over kv head
+        h // (Hq / Hkv).  The decode call of Attention.forward
+        (flash_attn_with_kvcache, attention.py:122-130) with the numerics of
+        SDPAAttention's decode branch (attention.py:284-300), without the
+        gather.  q [B, Hq, 128] bf16 -> [B, Hq, 128] bf16."""
+        validate_varlen_inputs(key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens)
+        if q.ndim != 3 or q.shape[0] != block_tables.shape[0]:
+            raise ValueError("q must be [num_seqs, num_q_heads, head_dim] with one row per sequence")
+        if q.device != key_cache.device:
+            raise ValueError("q and the caches must be on the same device")
+        self._load()
+        if plan is None:
+            plan = self.build_attention_plan(key_cache, block_tables, cu_seqlens_k, total_tokens)
+        if out is None:
+            out = torch.empty_like(q)
+        torch.ops.nanovllm_paged_kv.paged_attention_decode(
+            q, key_cache, value_cache, plan[0], plan[1], float(softmax_scale), out
+        )
+        return out
+
+
 def validate_varlen_inputs(
     key_cache: torch.Tensor,
     value_cache: torch.Tensor,

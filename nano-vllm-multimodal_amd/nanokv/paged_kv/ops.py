@@ -20,6 +20,12 @@ too, paged_kv_cuda.cu:168-171).  Additive ops, with no reference schema:
                       int row_elems, ScalarType dtype) -> Tensor
     gather_varlen_planned(Tensor key_cache, Tensor value_cache, Tensor plan,
                           Tensor(a!) key_out, Tensor(b!) value_out) -> ()
+    build_attention_plan(Tensor block_tables, Tensor cu_seqlens_k,
+                         int total_tokens, int num_blocks, int block_size)
+                         -> (Tensor, Tensor)
+    paged_attention_decode(Tensor q, Tensor key_cache, Tensor value_cache,
+                           Tensor plan, Tensor first_part, float scale,
+                           Tensor(a!) out) -> ()
 
 Every kernel runs on the current stream of the tensors' device and returns
 before it completes, like the reference ops.
@@ -45,6 +51,10 @@ SCHEMAS = {
     "ScalarType dtype) -> Tensor",
     "gather_varlen_planned": "gather_varlen_planned(Tensor key_cache, Tensor value_cache, "
     "Tensor plan, Tensor(a!) key_out, Tensor(b!) value_out) -> ()",
+    "build_attention_plan": "build_attention_plan(Tensor block_tables, Tensor cu_seqlens_k, "
+    "int total_tokens, int num_blocks, int block_size) -> (Tensor, Tensor)",
+    "paged_attention_decode": "paged_attention_decode(Tensor q, Tensor key_cache, "
+    "Tensor value_cache, Tensor plan, Tensor first_part, float scale, Tensor(a!) out) -> ()",
 }
 
 DTYPE_CODES = {
@@ -214,6 +224,62 @@ def _gather_varlen_impl(key_cache, value_cache, block_tables, cu_seqlens_k, tota
     return key_out, value_out
 
 
+def _build_attention_plan_impl(block_tables, cu_seqlens_k, total_tokens: int, num_blocks: int,
+                               block_size: int):
+    device = _require_device("paged KV HIP attention plan", block_tables, cu_seqlens_k)
+    num_seqs = cu_seqlens_k.numel() - 1
+    library = _lib.load_library()
+    capacity = int(library.nkv_attention_plan_capacity(total_tokens, num_seqs, block_size))
+    plan = torch.zeros((capacity, 4), dtype=torch.int32, device=device)
+    first_part = torch.empty(num_seqs + 1, dtype=torch.int32, device=device)
+    status = library.nkv_build_attention_plan(
+        block_tables.data_ptr(),
+        block_tables.stride(0) if block_tables.ndim == 2 else 0,
+        cu_seqlens_k.data_ptr(),
+        num_seqs,
+        block_size,
+        num_blocks,
+        plan.data_ptr() if capacity else None,
+        capacity,
+        first_part.data_ptr(),
+        _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::build_attention_plan")
+    return plan, first_part
+
+
+def _paged_attention_decode_impl(q, key_cache, value_cache, plan, first_part, scale: float, out) -> None:
+    device = _require_device(
+        "paged KV HIP attention", q, key_cache, value_cache, plan, first_part, out
+    )
+    _require_contiguous_cache("paged KV HIP attention", key_cache, value_cache)
+    if q.dtype != torch.bfloat16 or key_cache.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
+        raise ValueError("paged attention decode supports bfloat16 q, caches and output")
+    if q.ndim != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
+        raise ValueError("q must be [num_seqs, num_q_heads, head_dim] with contiguous heads")
+    if out.shape != q.shape or out.stride(2) != 1 or out.stride(1) != out.shape[2]:
+        raise ValueError("out must match q's shape with contiguous heads")
+    num_blocks, block_size, num_kv_heads, head_dim = key_cache.shape
+    if q.shape[2] != head_dim:
+        raise ValueError("q head_dim does not match the cache")
+    if plan.dtype != torch.int32 or plan.ndim != 2 or plan.shape[1] != 4 or not plan.is_contiguous():
+        raise ValueError("attention plan must be a contiguous [capacity, 4] int32 tensor")
+    if first_part.dtype != torch.int32 or first_part.numel() != q.shape[0] + 1:
+        raise ValueError("first_part must be int32 with num_seqs + 1 entries")
+    library = _lib.load_library()
+    capacity = plan.shape[0]
+    nbytes = int(library.nkv_attention_workspace_bytes(capacity, q.shape[1], head_dim))
+    workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+    status = library.nkv_paged_attention_decode(
+        q.data_ptr(), q.stride(0), key_cache.data_ptr(), value_cache.data_ptr(),
+        plan.data_ptr() if capacity else None, capacity, first_part.data_ptr(), q.shape[0],
+        num_kv_heads, q.shape[1], head_dim, block_size, num_blocks, float(scale),
+        _lib.NKV_DTYPE_BFLOAT16, workspace.data_ptr(), workspace.numel(), out.data_ptr(),
+        out.stride(0), _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::paged_attention_decode")
+
+
 def register_ops() -> None:
     """Define the schemas (unless another library already did) and register
     the HIP implementations on the CUDA key.  Idempotent."""
@@ -231,4 +297,6 @@ def register_ops() -> None:
         fragment.impl("gather_varlen", _gather_varlen_impl, "CUDA")
         fragment.impl("build_gather_plan", _build_plan_impl, "CUDA")
         fragment.impl("gather_varlen_planned", _gather_planned_impl, "CUDA")
+        fragment.impl("build_attention_plan", _build_attention_plan_impl, "CUDA")
+        fragment.impl("paged_attention_decode", _paged_attention_decode_impl, "CUDA")
         _FRAGMENT = fragment

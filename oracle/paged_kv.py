@@ -59,6 +59,40 @@ def gather_varlen(cache, block_tables, context_lens):
     return np.concatenate(parts, axis=0)
 
 
+def bf16_words_to_f32(words) -> np.ndarray:
+    """bf16 bit patterns (int16/uint16 words) -> float32 values (exact)."""
+    w = np.asarray(words).astype(np.uint16).astype(np.uint32)
+    return (w << 16).view(np.float32)
+
+
+def paged_attention_decode(q, key_cache, value_cache, block_tables, context_lens, scale: float):
+    """SDPAAttention's decode branch in float32 (nanovllm/layers/attention.py:
+    284-300): per request, gather K and V of its context (the pytorch
+    backend's gather, pytorch_backend.py:40-50), then
+    softmax(scale * q K^T) V with grouped-query heads: query head h reads kv
+    head h // (Hq / Hkv), as scaled_dot_product_attention(enable_gqa=True)
+    does (attention.py:194-203).  q [B, Hq, D] float32; caches hold bf16
+    words ([NB, BS, Hkv, D] int16); an empty context yields zeros."""
+    q = np.asarray(q, dtype=np.float32)
+    b, hq, d = q.shape
+    hkv = key_cache.shape[2]
+    group = hq // hkv
+    out = np.zeros((b, hq, d), dtype=np.float32)
+    for i, length in enumerate(np.asarray(context_lens).tolist()):
+        if length == 0:
+            continue
+        k = bf16_words_to_f32(gather(key_cache, block_tables[i], int(length)))
+        v = bf16_words_to_f32(gather(value_cache, block_tables[i], int(length)))
+        for h in range(hq):
+            kv = h // group
+            scores = (k[:, kv, :] @ q[i, h]) * np.float32(scale)
+            scores = scores - scores.max()
+            p = np.exp(scores)
+            p /= p.sum()
+            out[i, h] = p @ v[:, kv, :]
+    return out
+
+
 # --------------------------------------------------------------------- packing
 
 @dataclass
@@ -223,6 +257,8 @@ def gather_bruteforce(cache, block_table, sequence_length: int):
 
 __all__ = [
     "SeqState",
+    "bf16_words_to_f32",
+    "paged_attention_decode",
     "csr",
     "effective_bytes",
     "gather",
