@@ -248,27 +248,33 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  *   122-130); numerically the decode branch of SDPAAttention
  *   (attention.py:284-300: per-request gather, then SDPA with GQA).
  *
- * nkv_build_attention_plan writes one int4 entry per (sequence, cache
- *   block) into `plan` (capacity >= nkv_attention_plan_capacity(total
- *   context tokens, num_seqs, block_size)) and each sequence's first entry
- *   into first_part [num_seqs+1]; one plan serves every layer of a step.
+ * nkv_build_attention_plan cuts every context into entries of
+ *   nkv_attention_entry_rows(block_size) rows (whole blocks, 512 rows by
+ *   default) and writes one int4 {row0, rows, seq, 0} per entry into `plan`
+ *   (capacity >= nkv_attention_plan_capacity(total context tokens,
+ *   num_seqs, block_size)) and each sequence's first entry into first_part
+ *   [num_seqs+1].  It reads only cu_seqlens_k, so one plan serves every
+ *   layer of a step and stays valid while the context lengths do.
  * nkv_paged_attention_decode runs the split-K partial kernel and the
- *   merge; workspace holds nkv_attention_workspace_bytes(capacity,
- *   num_q_heads, head_dim) bytes (16-byte aligned).  q is [num_seqs,
- *   num_q_heads, head_dim] with row stride q_seq_stride elements; out is
- *   [num_seqs, num_q_heads, head_dim] with row stride out_seq_stride.
+ *   merge; block_tables [num_seqs, table_stride] (int32, -1 padded) map
+ *   context rows to cache blocks, a block id outside [0, num_blocks) or a
+ *   row past the table drops its rows; workspace holds
+ *   nkv_attention_workspace_bytes(capacity, num_q_heads, head_dim) bytes
+ *   (16-byte aligned).  q is [num_seqs, num_q_heads, head_dim] with row
+ *   stride q_seq_stride elements; out is [num_seqs, num_q_heads, head_dim]
+ *   with row stride out_seq_stride (even).
  */
+int64_t nkv_attention_entry_rows(int64_t block_size);
 int64_t nkv_attention_plan_capacity(int64_t total_tokens, int64_t num_seqs,
                                     int64_t block_size);
 int64_t nkv_attention_workspace_bytes(int64_t capacity, int64_t num_q_heads,
                                       int64_t head_dim);
-int nkv_build_attention_plan(const int32_t* block_tables, int64_t table_stride,
-                             const int32_t* cu_seqlens_k, int64_t num_seqs,
-                             int64_t block_size, int64_t num_blocks, void* plan,
-                             int64_t capacity, int32_t* first_part,
-                             void* stream);
+int nkv_build_attention_plan(const int32_t* cu_seqlens_k, int64_t num_seqs,
+                             int64_t block_size, void* plan, int64_t capacity,
+                             int32_t* first_part, void* stream);
 int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
                                const void* key_cache, const void* value_cache,
+                               const int32_t* block_tables, int64_t table_stride,
                                const void* plan, int64_t capacity,
                                const int32_t* first_part, int64_t num_seqs,
                                int64_t num_kv_heads, int64_t num_q_heads,

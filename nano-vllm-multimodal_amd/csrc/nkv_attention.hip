@@ -7,23 +7,27 @@
 // (attention.py:284-300: gather, then scaled_dot_product_attention with
 // enable_gqa, query head j reading kv head j / (Hq / Hkv)).
 //
-// Split-K ("flash decoding"): one workgroup per (sequence, cache block)
-// computes, for every query head, the block's softmax partials
-// (running max m, sum l, unnormalised output acc), and a reduce kernel
-// merges the partials of each (sequence, query head).
+// Split-K ("flash decoding"): the context of every sequence is cut into
+// entries of up to attention_entry_rows(block_size) rows (512 by default,
+// whole blocks), one workgroup per entry computes softmax partials for every
+// query head (reference max m, weight sum l, unnormalised output), and a
+// reduce kernel merges the partials of each (sequence, query head).
 //
-// Mapping inside a workgroup (256 threads, head_dim 128, bf16):
+// Mapping inside a workgroup (4 waves, head_dim 128, bf16):
+//   * the entry's cache rows are resolved once through the block table into
+//     LDS (invalid block ids give rows that are skipped);
 //   * a 16-lane DPP row owns one (row, kv head): each lane holds 8 dims
 //     (16 bytes), so a wavefront instruction reads 1 KiB of consecutive
-//     cache bytes (coalesced, non-temporal);
+//     cache bytes (coalesced, non-temporal); the waves take interleaved
+//     groups of rows, so the workgroup sweeps its rows as one front;
 //   * q.k for the G = Hq/Hkv query heads of that kv head is 4 v_dot2 on
 //     packed bf16 pairs plus a 4-step DPP row sum (fp32);
-//   * an online softmax in fp32 with exp2 (scale * log2 e folded in),
-//     updated once per 4 rows per wave;
-//   * the 4 waves split the block's rows and merge their partials in LDS.
-// Decode attention moves ~2 bytes per FLOP pair and has only G = 2..8 query
+//   * an online softmax in fp32 with exp2 (scale * log2 e folded in);
+//   * the waves merge in LDS without a barrier: the last one to arrive
+//     stores the entry's partials (fp16 sums with a power-of-two scale).
+// Decode attention moves ~2 bytes per FLOP pair and has only G = 1..8 query
 // rows per kv head, so it is bound by HBM reads; an MFMA tile (16 rows)
-// would idle 75-94% of its lanes, while the VALU work here is well under the
+// would idle most of its lanes, while the VALU work here stays under the
 // memory time and overlaps it across waves.
 #include <cmath>
 
@@ -32,14 +36,58 @@
 namespace nkv {
 namespace {
 
-constexpr int kAttnThreads = 256;
-constexpr int kAttnWaves = kAttnThreads / kWave;
+// Launch-shape knobs (compile-time; the defaults are the measured best on
+// MI355X for the 256-sequence decode step).
+#ifndef NKV_ATTN_WAVES
+#define NKV_ATTN_WAVES 4  // wavefronts per workgroup
+#endif
+#ifndef NKV_ATTN_UNROLL
+#define NKV_ATTN_UNROLL 4  // row loads in flight per lane per iteration
+#endif
+#ifndef NKV_ATTN_ENTRY_ROWS
+#define NKV_ATTN_ENTRY_ROWS 512  // target context rows per workgroup
+#endif
+#ifndef NKV_ATTN_NT_LOADS
+#define NKV_ATTN_NT_LOADS 1  // non-temporal K/V loads
+#endif
+
+constexpr int kAttnWaves = NKV_ATTN_WAVES;
+constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kHeadDim = 128;
 constexpr int kHeadBytes = kHeadDim * 2;  // bf16
-constexpr int kAttnUnroll = 4;
+constexpr int kAttnUnroll = NKV_ATTN_UNROLL;
 constexpr int kMaxQHeads = 16;
+constexpr int kEntryRows = NKV_ATTN_ENTRY_ROWS;
+constexpr int kMaxEntryBlocks = 64;  // blocks one entry may span
+constexpr int kPlanThreads = 1024;
+static_assert(kAttnWaves == 1 || kAttnWaves == 2 || kAttnWaves == 4 || kAttnWaves == 8,
+              "NKV_ATTN_WAVES must be 1, 2, 4 or 8");
+static_assert(kAttnUnroll >= 1 && kAttnUnroll <= 8, "NKV_ATTN_UNROLL must be in [1, 8]");
+static_assert(kEntryRows >= 1 && kEntryRows <= 4096, "NKV_ATTN_ENTRY_ROWS must be in [1, 4096]");
+
+// The running max is a reference, moved only when a score exceeds it by more
+// than this (log2 units): weights stay <= 2^8, far from fp32 overflow, and
+// the rescale of the accumulators (divergent across the heads of a wave)
+// becomes rare.  The final merge divides by the sum taken against the same
+// reference, so the result is the softmax up to rounding.
+constexpr float kRescaleLog2 = 8.f;
+
+// Context rows per plan entry: whole blocks up to NKV_ATTN_ENTRY_ROWS (at
+// most kMaxEntryBlocks of them, at least one), or, for blocks larger than
+// that, the largest divisor of the block that fits.
+int64_t attention_entry_rows(int64_t block_size) {
+  if (block_size <= kEntryRows) {
+    int64_t blocks = kEntryRows / block_size;
+    if (blocks > kMaxEntryBlocks) blocks = kMaxEntryBlocks;
+    return blocks * block_size;
+  }
+  int64_t rows = kEntryRows;
+  while (rows > 1 && block_size % rows != 0) --rows;
+  return rows;
+}
 
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // One v_dot2 on a packed bf16 pair.  The words arrive as scalars on purpose:
 // __builtin_bit_cast applied directly to an ext_vector component (a.y) is
@@ -70,6 +118,13 @@ __device__ __forceinline__ float row16_sum(float v) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xFFFFu)));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
 // fp32 -> bf16, round to nearest even (NaN stays a quiet NaN).
 __device__ __forceinline__ uint16_t to_bf16(float f) {
   uint32_t u = __float_as_uint(f);
@@ -80,29 +135,88 @@ __device__ __forceinline__ uint16_t to_bf16(float f) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Plan entry (from launch_block_plan with chunk_rows = block_size):
-// x = first cache row of the block (-1 if the block id is invalid), y = the
-// rows' offset in the sequence's context (unused), z = rows, w = sequence.
+// Plan: one int4 {row0, rows, seq, 0} per entry, rows [row0, row0 + rows)
+// of sequence seq's context, entries of a sequence consecutive;
+// first_part[i] is sequence i's first entry (first_part[num_seqs] = total).
+// Every workgroup rescans the per-sequence entry counts in LDS, so one
+// launch builds the whole plan.  Entries past the total get rows = 0.
+__global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(
+    const int32_t* __restrict__ cu_seqlens, int32_t num_seqs, int32_t entry_rows,
+    int4* __restrict__ plan, int64_t capacity, int32_t* __restrict__ first_part) {
+  extern __shared__ int32_t s_mem[];
+  int32_t* s_first = s_mem;               // [num_seqs + 1]
+  int32_t* s_tmp = s_mem + num_seqs + 1;  // [kPlanThreads / 64 + 1]
+  lds_exclusive_scan<kPlanThreads>(
+      num_seqs,
+      [&](int32_t i) {
+        const int32_t len = cu_seqlens[i + 1] - cu_seqlens[i];
+        return len > 0 ? (len + entry_rows - 1) / entry_rows : 0;
+      },
+      s_first, s_tmp);
+  if (blockIdx.x == 0) {
+    for (int32_t i = threadIdx.x; i <= num_seqs; i += kPlanThreads) first_part[i] = s_first[i];
+  }
+  const int64_t total = s_first[num_seqs];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; e < capacity;
+       e += stride) {
+    int4 entry = make_int4(0, 0, 0, 0);
+    if (e < total) {
+      const int32_t i = owner_of(s_first, num_seqs, static_cast<int32_t>(e));
+      const int32_t row0 = (static_cast<int32_t>(e) - s_first[i]) * entry_rows;
+      const int32_t len = cu_seqlens[i + 1] - cu_seqlens[i];
+      entry = make_int4(row0, min(entry_rows, len - row0), i, 0);
+    }
+    plan[e] = entry;
+  }
+}
+
+// Shared state of one workgroup: the entry's cache rows, each wave's
+// partials, and the count of waves that have published theirs.
+template <int HQ>
+struct AttnShared {
+  int32_t rows[kEntryRows];
+  float acc[kAttnWaves][HQ][kHeadDim];
+  float m[kAttnWaves][HQ];
+  float l[kAttnWaves][HQ];
+  uint32_t arrived;
+};
+
+// Partials of plan entry blockIdx.x, for every query head qh:
+//   part_acc[entry][qh][d/2] = fp16 pair of sum_rows p * v[d] * 2^-k,
+//   part_ml[entry][qh] = (m + k, l * 2^-k),
+// with p = 2^(score - m) against the reference max m (log2 units), l the
+// sum of the p, and k a per-head power of two that puts the largest
+// magnitude in [2^14, 2^15) (a 12-bit mantissa for every value well above
+// 2^-27 of the largest, no fp16 overflow).  Folding k into both m and l
+// keeps the merge exact: both sums carry the same factor 2^(m + k - M).
+// An entry without valid rows gives (-inf, 0) and zeros.
+//
+// Epilogue without a barrier: each wave publishes its partials in LDS and
+// bumps an arrival counter; the last wave to arrive merges and stores them,
+// the others exit at once, so their slots go to the next workgroup instead
+// of idling until the slowest wave's loads return.
 template <int HKV, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_seq_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
-    const int4* __restrict__ plan, int32_t num_seqs, int64_t cache_rows,
-    int32_t block_size, float scale_log2, float* __restrict__ part_acc,
-    float2* __restrict__ part_ml) {
+    const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,
+    int32_t num_blocks, const int4* __restrict__ plan, int32_t num_seqs, float scale_log2,
+    uint32_t* __restrict__ part_acc, f32x2* __restrict__ part_ml) {
   constexpr int HQ = HKV * G;
   constexpr int NC = HKV >= 4 ? HKV / 4 : 1;   // kv heads per lane per row
   constexpr int TPI = HKV >= 4 ? 1 : 4 / HKV;  // rows per wavefront load
   constexpr int kRowBytes = HKV * kHeadBytes;
   static_assert(HQ <= kMaxQHeads && NC * G <= 8, "unsupported head layout");
+  __shared__ AttnShared<HQ> sh;
 
-  const int4 entry = plan[blockIdx.x];
-  const int32_t nrows = entry.z;
-  const int32_t seq = entry.w;
-  if (nrows <= 0 || seq < 0 || seq >= num_seqs) return;
-  const int64_t src_row = entry.x;
-  const bool block_ok = src_row >= 0 && src_row + nrows <= cache_rows;
-  const int32_t valid_rows = block_ok ? nrows : 0;
+  const int64_t part = blockIdx.x;
+  const int4 entry = plan[part];
+  const int32_t row0 = entry.x;
+  const int32_t seq = entry.z;
+  // Uniform exits; an empty cache (num_blocks == 0) has no row to read.
+  if (entry.y <= 0 || seq < 0 || seq >= num_seqs || row0 < 0) return;
+  const int32_t nrows = num_blocks > 0 ? min(entry.y, kEntryRows) : 0;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -110,6 +224,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
   const int sub = lane & 15;
   const int head0 = HKV >= 4 ? slot : slot % HKV;
   const int row_off = HKV >= 4 ? 0 : slot / HKV;
+
+  // Cache row of every context row of the entry, -1 where the block id is
+  // missing from the table or outside the cache.
+  for (int32_t t = threadIdx.x; t < nrows; t += kAttnThreads) {
+    const int32_t ctx = row0 + t;
+    const int32_t logical = ctx / block_size;
+    int32_t cache_row = -1;
+    if (logical < table_stride) {
+      const int32_t block = tables[static_cast<int64_t>(seq) * table_stride + logical];
+      if (block >= 0 && block < num_blocks) cache_row = block * block_size + ctx % block_size;
+    }
+    sh.rows[t] = cache_row;
+  }
+  if (threadIdx.x == 0) sh.arrived = 0u;
+  __syncthreads();  // rows resolved, counter zero, before any wave reads or arrives
 
   u32x4 qf[NC][G];
   const uint16_t* qs = q + static_cast<int64_t>(seq) * q_seq_stride;
@@ -134,30 +263,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     }
   }
 
-  // Rows [r_begin, r_end) of the block belong to this wave (multiples of TPI).
-  const int32_t per_wave =
-      (block_size + kAttnWaves * TPI - 1) / (kAttnWaves * TPI) * TPI;
-  const int32_t r_begin = wave * per_wave;
-  const int32_t r_end = min(valid_rows, r_begin + per_wave);
-  const uint8_t* kb = key_cache + (block_ok ? src_row : 0) * kRowBytes;
-  const uint8_t* vb = value_cache + (block_ok ? src_row : 0) * kRowBytes;
-
-  for (int32_t r = r_begin; r < r_end; r += TPI * kAttnUnroll) {
+  // Each iteration a wave takes kAttnUnroll * TPI consecutive rows, and the
+  // waves' groups are adjacent, so the workgroup sweeps its rows as one
+  // front.
+  constexpr int32_t kGroupRows = kAttnUnroll * TPI;
+  for (int32_t r = wave * kGroupRows; r < nrows; r += kAttnWaves * kGroupRows) {
     u32x4 kw[kAttnUnroll][NC], vw[kAttnUnroll][NC];
     bool ok[kAttnUnroll];
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
-      const int32_t row_base = r + u * TPI;
-      ok[u] = row_base + row_off < r_end;
+      const int32_t t = r + u * TPI + row_off;
+      const int32_t cache_row = t < nrows ? sh.rows[t] : -1;
+      ok[u] = cache_row >= 0;
+      // A skipped row re-reads cache row 0 (in bounds: the cache is not
+      // empty here) and gets a -inf score, i.e. zero weight.
+      const int64_t safe_row = ok[u] ? cache_row : 0;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        kw[u][c] = u32x4{0u, 0u, 0u, 0u};
-        vw[u][c] = u32x4{0u, 0u, 0u, 0u};
-        if (ok[u]) {
-          const int64_t off = static_cast<int64_t>(row_base) * kRowBytes + c * 1024 + lane * 16;
-          kw[u][c] = load_stream(reinterpret_cast<const u32x4*>(kb + off));
-          vw[u][c] = load_stream(reinterpret_cast<const u32x4*>(vb + off));
-        }
+        const int64_t off = safe_row * kRowBytes + (HKV >= 4 ? c * 1024 + lane * 16
+                                                            : (lane & (16 * HKV - 1)) * 16);
+#if NKV_ATTN_NT_LOADS
+        kw[u][c] = load_stream(reinterpret_cast<const u32x4*>(key_cache + off));
+        vw[u][c] = load_stream(reinterpret_cast<const u32x4*>(value_cache + off));
+#else
+        kw[u][c] = *reinterpret_cast<const u32x4*>(key_cache + off);
+        vw[u][c] = *reinterpret_cast<const u32x4*>(value_cache + off);
+#endif
       }
     }
     float s[kAttnUnroll][NC][G];
@@ -191,16 +322,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
         float mt = s[0][c][g];
 #pragma unroll
         for (int u = 1; u < kAttnUnroll; ++u) mt = fmaxf(mt, s[u][c][g]);
-        const float m_new = fmaxf(m[c][g], mt);
-        if (m_new == -INFINITY) continue;  // nothing valid yet for this row
-        const float corr = exp2_fast(m[c][g] - m_new);
-        l[c][g] *= corr;
+        // Also taken for the first valid rows (m = -inf, corr = 0).
+        if (mt > m[c][g] + kRescaleLog2) {
+          const float corr = exp2_fast(m[c][g] - mt);
+          l[c][g] *= corr;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[c][g][j] *= corr;
-        m[c][g] = m_new;
+          for (int j = 0; j < 8; ++j) acc[c][g][j] *= corr;
+          m[c][g] = mt;
+        }
+        if (m[c][g] == -INFINITY) continue;  // nothing valid yet for this row
+        const float m_ref = m[c][g];
 #pragma unroll
         for (int u = 0; u < kAttnUnroll; ++u) {
-          const float p = exp2_fast(s[u][c][g] - m_new);
+          const float p = exp2_fast(s[u][c][g] - m_ref);
           l[c][g] += p;
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[c][g][j] = fmaf(p, v[u][j], acc[c][g][j]);
@@ -235,9 +369,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
     }
   }
 
-  __shared__ float s_acc[kAttnWaves][HQ][kHeadDim];
-  __shared__ float s_m[kAttnWaves][HQ];
-  __shared__ float s_l[kAttnWaves][HQ];
   if (row_off == 0) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -245,63 +376,126 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
       for (int g = 0; g < G; ++g) {
         const int qh = (head0 + 4 * c) * G + g;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s_acc[wave][qh][sub * 8 + j] = acc[c][g][j];
+        for (int j = 0; j < 8; ++j) sh.acc[wave][qh][sub * 8 + j] = acc[c][g][j];
         if (sub == 0) {
-          s_m[wave][qh] = m[c][g];
-          s_l[wave][qh] = l[c][g];
+          sh.m[wave][qh] = m[c][g];
+          sh.l[wave][qh] = l[c][g];
         }
       }
     }
   }
-  __syncthreads();
-  const int64_t part = blockIdx.x;
-  for (int idx = threadIdx.x; idx < HQ * kHeadDim; idx += kAttnThreads) {
-    const int qh = idx / kHeadDim;
-    const int d = idx - qh * kHeadDim;
+  // Publish (release), count the arrival; the wave that arrives last sees
+  // every other wave's partials after the acquire.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  uint32_t before = 0u;
+  if (lane == 0) {
+    before = __hip_atomic_fetch_add(&sh.arrived, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  before = __builtin_amdgcn_readfirstlane(before);
+  if (before != kAttnWaves - 1) return;  // whole wavefront; no barrier follows
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+  // Per query head, two dims per lane: merge the waves against the largest
+  // reference, scale, store.
+  for (int qh = 0; qh < HQ; ++qh) {
     float mm = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) mm = fmaxf(mm, s_m[w][qh]);
-    float a = 0.f, lsum = 0.f;
+    for (int w = 0; w < kAttnWaves; ++w) mm = fmaxf(mm, sh.m[w][qh]);
+    float a0 = 0.f, a1 = 0.f, lsum = 0.f;
     if (mm != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kAttnWaves; ++w) {
-        const float f = exp2_fast(s_m[w][qh] - mm);
-        a = fmaf(s_acc[w][qh][d], f, a);
-        lsum = fmaf(s_l[w][qh], f, lsum);
+        const float f = exp2_fast(sh.m[w][qh] - mm);
+        a0 = fmaf(sh.acc[w][qh][2 * lane], f, a0);
+        a1 = fmaf(sh.acc[w][qh][2 * lane + 1], f, a1);
+        lsum = fmaf(sh.l[w][qh], f, lsum);
       }
     }
-    part_acc[(part * HQ + qh) * kHeadDim + d] = a;
-    if (d == 0) part_ml[part * HQ + qh] = make_float2(mm, lsum);
+    float amax = fmaxf(fabsf(a0), fabsf(a1));
+#pragma unroll
+    for (int x = kWave / 2; x > 0; x >>= 1) amax = fmaxf(amax, __shfl_xor(amax, x, kWave));
+    const int e = static_cast<int>((__float_as_uint(amax) >> 23) & 0xFFu) - 127;
+    const int k = amax > 0.f ? min(112, max(-112, e - 14)) : 0;
+    const float down = __uint_as_float(static_cast<uint32_t>(127 - k) << 23);
+    const uint32_t packed =
+        static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a0 * down))) |
+        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a1 * down)))
+         << 16);
+    store_stream(part_acc + (part * HQ + qh) * (kHeadDim / 2) + lane, packed);
+    if (lane == 0) {
+      store_stream(part_ml + part * HQ + qh, f32x2{mm + static_cast<float>(k), lsum * down});
+    }
   }
 }
 
-// Merges the partials of one (sequence, query head): thread = one dim.
-__global__ __launch_bounds__(kHeadDim) void attn_decode_reduce_kernel(
-    const float* __restrict__ part_acc, const float2* __restrict__ part_ml,
+// Merges the partials of one (sequence, query head): the 4 waves of the
+// workgroup take the max of the parts' references together, then each walks
+// a quarter of the parts (two dims per lane from one fp16 pair, unrolled so
+// several loads are in flight), and wave 0 adds the four sums and divides
+// once.
+constexpr int kReduceWaves = 4;
+constexpr int kReduceThreads = kReduceWaves * kWave;
+
+__global__ __launch_bounds__(kReduceThreads) void attn_decode_reduce_kernel(
+    const uint32_t* __restrict__ part_acc, const f32x2* __restrict__ part_ml,
     const int32_t* __restrict__ first_part, int64_t capacity, int32_t num_q_heads,
     uint16_t* __restrict__ out, int64_t out_seq_stride) {
+  __shared__ float s_max[kReduceWaves];
+  __shared__ float s_acc[kReduceWaves][kHeadDim];
+  __shared__ float s_l[kReduceWaves];
   const int32_t seq = blockIdx.x;
   const int32_t qh = blockIdx.y;
-  const int32_t d = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
   const int64_t p0 = max(0, first_part[seq]);
   const int64_t p1 = min(capacity, static_cast<int64_t>(first_part[seq + 1]));
+
   float mm = -INFINITY;
-  for (int64_t p = p0; p < p1; ++p) mm = fmaxf(mm, part_ml[p * num_q_heads + qh].x);
-  float a = 0.f, lsum = 0.f;
+  for (int64_t p = p0 + threadIdx.x; p < p1; p += kReduceThreads) {
+    mm = fmaxf(mm, part_ml[p * num_q_heads + qh].x);
+  }
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) mm = fmaxf(mm, __shfl_xor(mm, d, kWave));
+  if (lane == 0) s_max[wave] = mm;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kReduceWaves; ++w) mm = fmaxf(mm, s_max[w]);
+
+  float ax = 0.f, ay = 0.f, lsum = 0.f;
   if (mm != -INFINITY) {
-    for (int64_t p = p0; p < p1; ++p) {
-      const float2 ml = part_ml[p * num_q_heads + qh];
+#pragma unroll 8
+    for (int64_t p = p0 + wave; p < p1; p += kReduceWaves) {
+      const f32x2 ml = part_ml[p * num_q_heads + qh];  // (m + k, l * 2^-k)
+      const uint32_t v = part_acc[(p * num_q_heads + qh) * (kHeadDim / 2) + lane];
       const float f = exp2_fast(ml.x - mm);
-      a = fmaf(part_acc[(p * num_q_heads + qh) * kHeadDim + d], f, a);
+      ax = fmaf(half_lo(v), f, ax);
+      ay = fmaf(half_hi(v), f, ay);
       lsum = fmaf(ml.y, f, lsum);
     }
   }
-  const float o = lsum > 0.f ? a / lsum : 0.f;
-  out[static_cast<int64_t>(seq) * out_seq_stride + qh * kHeadDim + d] = to_bf16(o);
+  s_acc[wave][2 * lane] = ax;
+  s_acc[wave][2 * lane + 1] = ay;
+  if (lane == 0) s_l[wave] = lsum;
+  __syncthreads();
+  if (wave != 0) return;  // no barrier follows
+  ax = ay = lsum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kReduceWaves; ++w) {
+    ax += s_acc[w][2 * lane];
+    ay += s_acc[w][2 * lane + 1];
+    lsum += s_l[w];
+  }
+  const bool any = lsum > 0.f;
+  const uint32_t packed = static_cast<uint32_t>(to_bf16(any ? ax / lsum : 0.f)) |
+                          (static_cast<uint32_t>(to_bf16(any ? ay / lsum : 0.f)) << 16);
+  *reinterpret_cast<uint32_t*>(out + static_cast<int64_t>(seq) * out_seq_stride +
+                               qh * kHeadDim + 2 * lane) = packed;
 }
 
 using PartialKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const uint8_t*,
-                               const int4*, int32_t, int64_t, int32_t, float, float*, float2*);
+                               const int32_t*, int64_t, int32_t, int32_t, const int4*, int32_t,
+                               float, uint32_t*, f32x2*);
 
 PartialKernel partial_kernel_for(int64_t hkv, int64_t g) {
 #define NKV_ATTN_CASE(H, GG) \
@@ -326,51 +520,58 @@ PartialKernel partial_kernel_for(int64_t hkv, int64_t g) {
 }  // namespace
 }  // namespace nkv
 
+extern "C" int64_t nkv_attention_entry_rows(int64_t block_size) {
+  return block_size > 0 ? nkv::attention_entry_rows(block_size) : 0;
+}
+
 extern "C" int64_t nkv_attention_plan_capacity(int64_t total_tokens, int64_t num_seqs,
                                                int64_t block_size) {
   if (total_tokens < 0 || num_seqs < 0 || block_size <= 0) return 0;
-  return (total_tokens + block_size - 1) / block_size + num_seqs;
+  const int64_t rows = nkv::attention_entry_rows(block_size);
+  return (total_tokens + rows - 1) / rows + num_seqs;
 }
 
 extern "C" int64_t nkv_attention_workspace_bytes(int64_t capacity, int64_t num_q_heads,
                                                  int64_t head_dim) {
   if (capacity < 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
-  return capacity * num_q_heads * (head_dim * 4 + 8);
+  // per (entry, query head): head_dim fp16 sums and a float2 (m + k, l * 2^-k)
+  return capacity * num_q_heads * (head_dim * 2 + 8);
 }
 
-extern "C" int nkv_build_attention_plan(const int32_t* block_tables, int64_t table_stride,
-                                        const int32_t* cu_seqlens_k, int64_t num_seqs,
-                                        int64_t block_size, int64_t num_blocks, void* plan,
-                                        int64_t capacity, int32_t* first_part,
-                                        void* stream) {
+extern "C" int nkv_build_attention_plan(const int32_t* cu_seqlens_k, int64_t num_seqs,
+                                        int64_t block_size, void* plan, int64_t capacity,
+                                        int32_t* first_part, void* stream) {
   using namespace nkv;
   if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_attention_plan: num_seqs=%lld outside [0, %d]",
                     static_cast<long long>(num_seqs), NKV_MAX_PLAN_SEQS);
   }
-  if (block_size <= 0 || num_blocks < 0 || num_blocks * block_size > INT32_MAX ||
-      capacity < 0 || capacity > INT32_MAX || table_stride < 0) {
-    return nkv_fail(NKV_E_INVALID, "nkv_build_attention_plan: bad geometry or capacity");
+  if (block_size <= 0 || block_size > INT32_MAX || capacity < 0 || capacity > INT32_MAX) {
+    return nkv_fail(NKV_E_INVALID, "nkv_build_attention_plan: bad block_size or capacity");
   }
-  if (!first_part || (num_seqs > 0 && (!block_tables || !cu_seqlens_k)) ||
-      (capacity > 0 && !plan)) {
+  if (!first_part || (num_seqs > 0 && !cu_seqlens_k) || (capacity > 0 && !plan)) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_attention_plan: null pointer");
   }
   if (reinterpret_cast<uint64_t>(plan) % 16 != 0) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_attention_plan: plan must be 16-byte aligned");
   }
-  return launch_block_plan(block_tables, table_stride, cu_seqlens_k, num_seqs, INT32_MAX,
-                           block_size, block_size, num_blocks, static_cast<int32_t*>(plan),
-                           capacity, first_part, static_cast<hipStream_t>(stream),
-                           "nkv_build_attention_plan");
+  const int64_t blocks = capacity > 0 ? (capacity + kPlanThreads - 1) / kPlanThreads : 1;
+  const size_t lds = (static_cast<size_t>(num_seqs) + 1 + kPlanThreads / kWave + 1) *
+                     sizeof(int32_t);
+  attn_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPlanThreads), lds,
+                     static_cast<hipStream_t>(stream)>>>(
+      cu_seqlens_k, static_cast<int32_t>(num_seqs),
+      static_cast<int32_t>(attention_entry_rows(block_size)), static_cast<int4*>(plan),
+      capacity, first_part);
+  return nkv_check_launch("nkv_build_attention_plan");
 }
 
 extern "C" int nkv_paged_attention_decode(
     const void* q, int64_t q_seq_stride, const void* key_cache, const void* value_cache,
-    const void* plan, int64_t capacity, const int32_t* first_part, int64_t num_seqs,
-    int64_t num_kv_heads, int64_t num_q_heads, int64_t head_dim, int64_t block_size,
-    int64_t num_blocks, float scale, int32_t dtype, void* workspace, int64_t workspace_bytes,
-    void* out, int64_t out_seq_stride, void* stream) {
+    const int32_t* block_tables, int64_t table_stride, const void* plan, int64_t capacity,
+    const int32_t* first_part, int64_t num_seqs, int64_t num_kv_heads, int64_t num_q_heads,
+    int64_t head_dim, int64_t block_size, int64_t num_blocks, float scale, int32_t dtype,
+    void* workspace, int64_t workspace_bytes, void* out, int64_t out_seq_stride, void* stream) {
   using namespace nkv;
   if (dtype != NKV_DTYPE_BFLOAT16) {
     return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: only bfloat16 is supported");
@@ -392,7 +593,8 @@ extern "C" int nkv_paged_attention_decode(
   }
   if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX ||
       block_size <= 0 || num_blocks < 0 || num_blocks * block_size > INT32_MAX ||
-      q_seq_stride < num_q_heads * head_dim || out_seq_stride < num_q_heads * head_dim) {
+      table_stride < 0 || q_seq_stride < num_q_heads * head_dim ||
+      out_seq_stride < num_q_heads * head_dim) {
     return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: bad sizes or strides");
   }
   if (!std::isfinite(scale)) {
@@ -405,31 +607,34 @@ extern "C" int nkv_paged_attention_decode(
                     "nkv_paged_attention_decode: workspace of %lld bytes < %lld needed",
                     static_cast<long long>(workspace_bytes), static_cast<long long>(need));
   }
-  if (!q || !key_cache || !value_cache || !first_part || !out || (capacity > 0 && (!plan || !workspace))) {
+  if (!q || !key_cache || !value_cache || !first_part || !out ||
+      (capacity > 0 && (!plan || !workspace || (table_stride > 0 && !block_tables)))) {
     return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: null pointer");
   }
   if ((reinterpret_cast<uint64_t>(q) | reinterpret_cast<uint64_t>(key_cache) |
        reinterpret_cast<uint64_t>(value_cache) | reinterpret_cast<uint64_t>(plan) |
        reinterpret_cast<uint64_t>(workspace) | static_cast<uint64_t>(q_seq_stride * 2)) % 16 != 0 ||
-      reinterpret_cast<uint64_t>(out) % 2 != 0) {
+      (reinterpret_cast<uint64_t>(out) | static_cast<uint64_t>(out_seq_stride * 2)) % 4 != 0) {
     return nkv_fail(NKV_E_INVALID,
-                    "nkv_paged_attention_decode: q/caches/plan/workspace must be 16-byte aligned");
+                    "nkv_paged_attention_decode: q/caches/plan/workspace must be 16-byte aligned "
+                    "and out rows 4-byte aligned");
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  auto* part_acc = static_cast<float*>(workspace);
-  auto* part_ml = reinterpret_cast<float2*>(part_acc + capacity * num_q_heads * head_dim);
+  auto* part_acc = static_cast<uint32_t*>(workspace);  // fp16 pairs
+  auto* part_ml = reinterpret_cast<f32x2*>(part_acc + capacity * num_q_heads * head_dim / 2);
   const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
   if (capacity > 0) {
     kernel<<<dim3(static_cast<unsigned>(capacity)), dim3(kAttnThreads), 0, s>>>(
         static_cast<const uint16_t*>(q), q_seq_stride, static_cast<const uint8_t*>(key_cache),
-        static_cast<const uint8_t*>(value_cache), static_cast<const int4*>(plan),
-        static_cast<int32_t>(num_seqs), num_blocks * block_size,
-        static_cast<int32_t>(block_size), scale_log2, part_acc, part_ml);
+        static_cast<const uint8_t*>(value_cache), block_tables, table_stride,
+        static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
+        static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2, part_acc,
+        part_ml);
     if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
   }
   attn_decode_reduce_kernel<<<dim3(static_cast<unsigned>(num_seqs),
                                    static_cast<unsigned>(num_q_heads)),
-                              dim3(kHeadDim), 0, s>>>(
+                              dim3(kReduceThreads), 0, s>>>(
       part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
       static_cast<uint16_t*>(out), out_seq_stride);
   return nkv_check_launch("nkv_paged_attention_decode (reduce)");

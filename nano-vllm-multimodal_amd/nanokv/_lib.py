@@ -60,17 +60,19 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
             c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
         ),
     ),
+    "nkv_attention_entry_rows": (c_i64, (c_i64,)),
     "nkv_attention_plan_capacity": (c_i64, (c_i64, c_i64, c_i64)),
     "nkv_attention_workspace_bytes": (c_i64, (c_i64, c_i64, c_i64)),
     "nkv_build_attention_plan": (
         ctypes.c_int,
-        (c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr),
+        (c_ptr, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr),
     ),
     "nkv_paged_attention_decode": (
         ctypes.c_int,
         (
-            c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64,
-            c_i64, c_i64, ctypes.c_float, c_i32, c_ptr, c_i64, c_ptr, c_i64, c_ptr,
+            c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i64,
+            c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_i32, c_ptr, c_i64, c_ptr, c_i64,
+            c_ptr,
         ),
     ),
     "nkv_transfer_create": (ctypes.c_int, (c_i32, c_ptr_out)),

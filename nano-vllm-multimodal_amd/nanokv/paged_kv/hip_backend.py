@@ -177,16 +177,16 @@ class HIPPagedKVBackend:
     def build_attention_plan(
         self,
         cache: torch.Tensor,
-        block_tables: torch.Tensor,
         cu_seqlens_k: torch.Tensor,
         total_tokens: int,
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """(plan, first_part) for :meth:`paged_attention_decode`: one entry
-        per (sequence, cache block); valid for every layer of the step."""
+        """(plan, first_part) for :meth:`paged_attention_decode`: each
+        context cut into entries of whole blocks (512 rows by default).  It
+        depends on the context lengths only, so one plan serves every layer
+        of a step (and every step with the same lengths)."""
         self._load()
-        num_blocks, block_size = cache.shape[:2]
         return torch.ops.nanovllm_paged_kv.build_attention_plan(
-            block_tables, cu_seqlens_k, total_tokens, num_blocks, block_size
+            cu_seqlens_k, total_tokens, cache.shape[1]
         )
 
     def paged_attention_decode(
@@ -216,11 +216,11 @@ class HIPPagedKVBackend:
             raise ValueError("q and the caches must be on the same device")
         self._load()
         if plan is None:
-            plan = self.build_attention_plan(key_cache, block_tables, cu_seqlens_k, total_tokens)
+            plan = self.build_attention_plan(key_cache, cu_seqlens_k, total_tokens)
         if out is None:
             out = torch.empty_like(q)
         torch.ops.nanovllm_paged_kv.paged_attention_decode(
-            q, key_cache, value_cache, plan[0], plan[1], float(softmax_scale), out
+            q, key_cache, value_cache, block_tables, plan[0], plan[1], float(softmax_scale), out
         )
         return out
 

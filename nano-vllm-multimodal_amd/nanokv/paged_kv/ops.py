@@ -20,11 +20,11 @@ too, paged_kv_cuda.cu:168-171).  Additive ops, with no reference schema:
                       int row_elems, ScalarType dtype) -> Tensor
     gather_varlen_planned(Tensor key_cache, Tensor value_cache, Tensor plan,
                           Tensor(a!) key_out, Tensor(b!) value_out) -> ()
-    build_attention_plan(Tensor block_tables, Tensor cu_seqlens_k,
-                         int total_tokens, int num_blocks, int block_size)
-                         -> (Tensor, Tensor)
+    build_attention_plan(Tensor cu_seqlens_k, int total_tokens,
+                         int block_size) -> (Tensor, Tensor)
     paged_attention_decode(Tensor q, Tensor key_cache, Tensor value_cache,
-                           Tensor plan, Tensor first_part, float scale,
+                           Tensor block_tables, Tensor plan,
+                           Tensor first_part, float scale,
                            Tensor(a!) out) -> ()
 
 Every kernel runs on the current stream of the tensors' device and returns
@@ -51,10 +51,11 @@ SCHEMAS = {
     "ScalarType dtype) -> Tensor",
     "gather_varlen_planned": "gather_varlen_planned(Tensor key_cache, Tensor value_cache, "
     "Tensor plan, Tensor(a!) key_out, Tensor(b!) value_out) -> ()",
-    "build_attention_plan": "build_attention_plan(Tensor block_tables, Tensor cu_seqlens_k, "
-    "int total_tokens, int num_blocks, int block_size) -> (Tensor, Tensor)",
+    "build_attention_plan": "build_attention_plan(Tensor cu_seqlens_k, int total_tokens, "
+    "int block_size) -> (Tensor, Tensor)",
     "paged_attention_decode": "paged_attention_decode(Tensor q, Tensor key_cache, "
-    "Tensor value_cache, Tensor plan, Tensor first_part, float scale, Tensor(a!) out) -> ()",
+    "Tensor value_cache, Tensor block_tables, Tensor plan, Tensor first_part, float scale, "
+    "Tensor(a!) out) -> ()",
 }
 
 DTYPE_CODES = {
@@ -224,21 +225,19 @@ def _gather_varlen_impl(key_cache, value_cache, block_tables, cu_seqlens_k, tota
     return key_out, value_out
 
 
-def _build_attention_plan_impl(block_tables, cu_seqlens_k, total_tokens: int, num_blocks: int,
-                               block_size: int):
-    device = _require_device("paged KV HIP attention plan", block_tables, cu_seqlens_k)
+def _build_attention_plan_impl(cu_seqlens_k, total_tokens: int, block_size: int):
+    device = _require_device("paged KV HIP attention plan", cu_seqlens_k)
+    if cu_seqlens_k.dtype != torch.int32 or cu_seqlens_k.ndim != 1 or not cu_seqlens_k.is_contiguous():
+        raise ValueError("cu_seqlens_k must be a contiguous 1-D int32 tensor")
     num_seqs = cu_seqlens_k.numel() - 1
     library = _lib.load_library()
     capacity = int(library.nkv_attention_plan_capacity(total_tokens, num_seqs, block_size))
-    plan = torch.zeros((capacity, 4), dtype=torch.int32, device=device)
+    plan = torch.empty((capacity, 4), dtype=torch.int32, device=device)
     first_part = torch.empty(num_seqs + 1, dtype=torch.int32, device=device)
     status = library.nkv_build_attention_plan(
-        block_tables.data_ptr(),
-        block_tables.stride(0) if block_tables.ndim == 2 else 0,
         cu_seqlens_k.data_ptr(),
         num_seqs,
         block_size,
-        num_blocks,
         plan.data_ptr() if capacity else None,
         capacity,
         first_part.data_ptr(),
@@ -248,10 +247,14 @@ def _build_attention_plan_impl(block_tables, cu_seqlens_k, total_tokens: int, nu
     return plan, first_part
 
 
-def _paged_attention_decode_impl(q, key_cache, value_cache, plan, first_part, scale: float, out) -> None:
+def _paged_attention_decode_impl(q, key_cache, value_cache, block_tables, plan, first_part,
+                                 scale: float, out) -> None:
     device = _require_device(
-        "paged KV HIP attention", q, key_cache, value_cache, plan, first_part, out
+        "paged KV HIP attention", q, key_cache, value_cache, block_tables, plan, first_part, out
     )
+    if (block_tables.dtype != torch.int32 or block_tables.ndim != 2
+            or block_tables.shape[0] != q.shape[0] or not block_tables.is_contiguous()):
+        raise ValueError("block_tables must be a contiguous [num_seqs, width] int32 tensor")
     _require_contiguous_cache("paged KV HIP attention", key_cache, value_cache)
     if q.dtype != torch.bfloat16 or key_cache.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
         raise ValueError("paged attention decode supports bfloat16 q, caches and output")
@@ -272,6 +275,7 @@ def _paged_attention_decode_impl(q, key_cache, value_cache, plan, first_part, sc
     workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
     status = library.nkv_paged_attention_decode(
         q.data_ptr(), q.stride(0), key_cache.data_ptr(), value_cache.data_ptr(),
+        block_tables.data_ptr(), block_tables.shape[1],
         plan.data_ptr() if capacity else None, capacity, first_part.data_ptr(), q.shape[0],
         num_kv_heads, q.shape[1], head_dim, block_size, num_blocks, float(scale),
         _lib.NKV_DTYPE_BFLOAT16, workspace.data_ptr(), workspace.numel(), out.data_ptr(),

@@ -81,7 +81,7 @@ def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):
     lens = [300, 1, 513, 256, 40]
     dev, host, total = build_case(gpu_device, 8, 2, 256, lens, seed=7, q_pad_heads=16)
     assert dev["q"].stride(0) == 32 * 128
-    plan = backend.build_attention_plan(dev["kc"], dev["tables"], dev["cu"], total)
+    plan = backend.build_attention_plan(dev["kc"], dev["cu"], total)
     out = torch.empty((len(lens), 16, 128), dtype=torch.bfloat16, device=gpu_device)
     ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], host["tables"],
                                         host["lens"], 0.1)
@@ -90,6 +90,60 @@ def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):
         backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev["tables"], dev["cu"],
                                        total, 0.1, plan=plan, out=out)
         check_close(out, ref, "planned")
+
+
+@pytest.mark.parametrize("hkv,g,bs", [(8, 2, 16), (2, 4, 8), (4, 2, 4), (1, 1, 1024)])
+def test_long_contexts_over_small_blocks(backend, gpu_device, hkv, g, bs):
+    """Entries span many blocks (512 rows of 8- or 16-row blocks, 256 rows =
+    64 blocks of 4 rows) or half of one (1024-row blocks); contexts of
+    several entries with ragged tails; the plan's entries tile each context
+    in order."""
+    from nanokv import _lib
+
+    rows = int(_lib.load_library().nkv_attention_entry_rows(bs))
+    lens = [3 * rows + 5, rows, rows + 1, 2 * rows - 1, 7, 1]
+    dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=hkv * 7 + g + bs)
+    plan, first = backend.build_attention_plan(dev["kc"], dev["cu"], total)
+    expect_entries = [-(-n // rows) for n in lens]
+    assert first.cpu().tolist() == [0] + np.cumsum(expect_entries).tolist()
+    entries = plan.cpu().numpy()[: sum(expect_entries)]
+    for i, n in enumerate(lens):
+        own = entries[entries[:, 2] == i]
+        assert own[:, 0].tolist() == list(range(0, n, rows))
+        assert int(own[:, 1].sum()) == n
+    out = backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev["tables"], dev["cu"],
+                                         total, 1 / math.sqrt(128), plan=(plan, first))
+    ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], host["tables"],
+                                        host["lens"], 1 / math.sqrt(128))
+    check_close(out, ref, f"hkv={hkv} g={g} bs={bs}")
+
+
+def test_invalid_block_ids_drop_their_rows(backend, gpu_device):
+    """A block id outside [0, num_blocks) (or -1) inside a context drops that
+    block's rows, so the result equals attention over the remaining rows;
+    the kernel never reads outside the cache."""
+    bs = 16
+    lens = [5 * bs, 3 * bs + 4, 2 * bs]
+    dev, host, total = build_case(gpu_device, 8, 2, bs, lens, seed=11)
+    nb = host["kc"].shape[0]
+    bad_tables = host["tables"].copy()
+    bad_tables[0, 2] = nb + 7      # out of range
+    bad_tables[1, 0] = -1          # negative
+    bad_tables[2, 1] = 2 ** 30     # far out of range
+    dev_tables = torch.from_numpy(bad_tables).to(gpu_device)
+    out = backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev_tables, dev["cu"],
+                                         total, 1 / math.sqrt(128))
+    # expected: the same contexts without the dropped (full) blocks
+    kept_tables = np.full_like(host["tables"], -1)
+    kept_lens = []
+    for i, n in enumerate(lens):
+        nblk = -(-n // bs)
+        keep = [host["tables"][i, j] for j in range(nblk) if 0 <= bad_tables[i, j] < nb]
+        kept_tables[i, : len(keep)] = keep
+        kept_lens.append(n - (nblk - len(keep)) * bs)
+    ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], kept_tables,
+                                        np.asarray(kept_lens), 1 / math.sqrt(128))
+    check_close(out, ref, "invalid blocks")
 
 
 def test_decode_step_layer_full_size(backend, gpu_device):
