@@ -249,7 +249,7 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  *   (attention.py:284-300: per-request gather, then SDPA with GQA).
  *
  * nkv_build_attention_plan cuts every context into entries of
- *   nkv_attention_entry_rows(block_size) rows (whole blocks, 512 rows by
+ *   nkv_attention_entry_rows(block_size) rows (whole blocks, 768 rows by
  *   default) and writes one int4 {row0, rows, seq, 0} per entry into `plan`
  *   (capacity >= nkv_attention_plan_capacity(total context tokens,
  *   num_seqs, block_size)) and each sequence's first entry into first_part

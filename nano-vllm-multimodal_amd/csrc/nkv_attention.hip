@@ -8,12 +8,12 @@
 // enable_gqa, query head j reading kv head j / (Hq / Hkv)).
 //
 // Split-K ("flash decoding"): the context of every sequence is cut into
-// entries of up to attention_entry_rows(block_size) rows (512 by default,
+// entries of up to attention_entry_rows(block_size) rows (768 by default,
 // whole blocks), one workgroup per entry computes softmax partials for every
 // query head (reference max m, weight sum l, unnormalised output), and a
 // reduce kernel merges the partials of each (sequence, query head).
 //
-// Mapping inside a workgroup (4 waves, head_dim 128, bf16):
+// Mapping inside a workgroup (8 waves, head_dim 128, bf16):
 //   * the entry's cache rows are resolved once through the block table into
 //     LDS (invalid block ids give rows that are skipped);
 //   * a 16-lane DPP row owns one (row, kv head): each lane holds 8 dims
@@ -39,16 +39,24 @@ namespace {
 // Launch-shape knobs (compile-time; the defaults are the measured best on
 // MI355X for the 256-sequence decode step).
 #ifndef NKV_ATTN_WAVES
-#define NKV_ATTN_WAVES 4  // wavefronts per workgroup
+#define NKV_ATTN_WAVES 8  // wavefronts per workgroup
 #endif
 #ifndef NKV_ATTN_UNROLL
 #define NKV_ATTN_UNROLL 4  // row loads in flight per lane per iteration
 #endif
 #ifndef NKV_ATTN_ENTRY_ROWS
-#define NKV_ATTN_ENTRY_ROWS 512  // target context rows per workgroup
+#define NKV_ATTN_ENTRY_ROWS 768  // target context rows per workgroup
 #endif
 #ifndef NKV_ATTN_NT_LOADS
 #define NKV_ATTN_NT_LOADS 1  // non-temporal K/V loads
+#endif
+#ifndef NKV_ATTN_WAVES_PER_EU
+#define NKV_ATTN_WAVES_PER_EU 0  // >0: ask for that many waves per SIMD (caps VGPRs)
+#endif
+#if NKV_ATTN_WAVES_PER_EU > 0
+#define NKV_ATTN_OCCUPANCY __attribute__((amdgpu_waves_per_eu(NKV_ATTN_WAVES_PER_EU)))
+#else
+#define NKV_ATTN_OCCUPANCY
 #endif
 
 constexpr int kAttnWaves = NKV_ATTN_WAVES;
@@ -197,7 +205,7 @@ struct AttnShared {
 // the others exit at once, so their slots go to the next workgroup instead
 // of idling until the slowest wave's loads return.
 template <int HKV, int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_partial_kernel(
+__global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_seq_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
     const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,

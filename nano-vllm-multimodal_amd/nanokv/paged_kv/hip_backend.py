@@ -181,7 +181,7 @@ class HIPPagedKVBackend:
         total_tokens: int,
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """(plan, first_part) for :meth:`paged_attention_decode`: each
-        context cut into entries of whole blocks (512 rows by default).  It
+        context cut into entries of whole blocks (768 rows by default).  It
         depends on the context lengths only, so one plan serves every layer
         of a step (and every step with the same lengths)."""
         self._load()
