@@ -14,12 +14,16 @@ Prints one JSON line:  value = store+gather algorithmic GB/s of the step
 (sum of the bytes the store and gather must move / step time), plus
 decode tokens/s, the HBM roofline of the dominant kernel (the varlen
 gather, timed live with events on its stream) and a CPU baseline (the
-oracle's C restatement on the host cores, bounded sample).
+oracle's C restatement on the host cores, bounded sample; the same leg
+checks the GPU outputs of --check-layers against the oracle).  A second
+timed step replaces the gather by its consumer, paged-attention decode read
+straight from the cache (16 query heads), reported under "attention".
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import platform
 import sys
 import time
@@ -122,42 +126,26 @@ def main(argv=None) -> int:
                 timer.stop(t0)
         return ctx
 
-    # ---------------------------------------------------------- correctness gate
-    check_layers = [int(x) for x in args.check_layers.split(",") if x.strip()] if not args.profile else []
-    if check_layers:
-        from oracle import c_oracle
+    # Decode attention straight from the paged cache (the consumer of the
+    # gathered K/V): Qwen3-VL-2B's language model has 16 query heads over the
+    # 8 kv heads.  Its plan depends on the context lengths only.
+    num_q_heads = 16
+    softmax_scale = 1.0 / math.sqrt(wl.head_dim)
+    q = torch.randn((B, num_q_heads, wl.head_dim), generator=g, device=device).to(wl.dtype)
+    attn_out = torch.empty_like(q)
 
-        tables = wl.padded_block_tables()
-        used = np.unique(tables[tables >= 0])
-        remap = np.full(wl.num_blocks, -1, np.int64)
-        remap[used] = np.arange(used.size)
-        index = torch.from_numpy(used.astype(np.int64)).to(device)
-        ctables = np.where(tables >= 0, remap[np.maximum(tables, 0)], -1).astype(np.int32)
-        cslots = (remap[wl.slot_mapping // wl.block_size] * wl.block_size
-                  + wl.slot_mapping % wl.block_size).astype(np.int32)
-        before = {}
-        for layer in check_layers:
-            before[layer] = [cache[kv, layer].index_select(0, index).cpu().view(torch.int16).numpy()
-                             for kv in range(2)]
+    def attention_step(timer: LaunchTimer | None = None):
         ctx = packer.pack_decode(batch)
-        plan = backend.build_gather_plan(cache[0, 0], ctx.block_tables, ctx.cu_seqlens_k, total)
-        cu = wl.cu_seqlens_k()
+        aplan = backend.build_attention_plan(cache[0, 0], ctx.cu_seqlens_k, total)
         for layer in range(L):
             kc, vc = cache[0, layer], cache[1, layer]
             backend.store(new_k[layer], new_v[layer], kc, vc, ctx.slot_mapping)
-            backend.gather_varlen(kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
-                                  plan=plan, out=(k_out, v_out))
-            if layer in before:
-                hk, hv = before[layer]
-                c_oracle.store(wl.key[layer].view(torch.int16).numpy(),
-                               wl.value[layer].view(torch.int16).numpy(), hk, hv, cslots,
-                               threads=c_oracle.default_threads())
-                for got, host in ((k_out, hk), (v_out, hv)):
-                    expected = c_oracle.gather_varlen(host, ctables, cu, threads=c_oracle.default_threads())
-                    if not np.array_equal(got.cpu().view(torch.int16).numpy(), expected):
-                        raise AssertionError(f"decode step layer {layer}: gather differs from the oracle")
-                log(f"[bench] correctness gate: layer {layer} store+gather bit-exact vs oracle")
-        torch.cuda.synchronize()
+            t0 = timer.start() if timer else None
+            backend.paged_attention_decode(q, kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
+                                           softmax_scale, plan=aplan, out=attn_out)
+            if timer:
+                timer.stop(t0)
+        return ctx
 
     # -------------------------------------------------------------- timed steps
     for _ in range(args.warmup):
@@ -177,6 +165,24 @@ def main(argv=None) -> int:
     wall_s = time.perf_counter() - t0
     step_ms = start_evt.elapsed_time(end_evt) / args.steps
     log(f"[bench] {args.steps} steps: {step_ms:.3f} ms/step (wall {wall_s * 1000 / args.steps:.3f})")
+
+    # Same step with the attention consumer instead of the gather.
+    for _ in range(args.warmup):
+        attention_step()
+    attn_timer = LaunchTimer(stream)
+    torch.cuda.synchronize()
+    start_evt.record(stream)
+    for _ in range(args.steps):
+        attention_step(attn_timer)
+    end_evt.record(stream)
+    torch.cuda.synchronize()
+    attn_step_ms = start_evt.elapsed_time(end_evt) / args.steps
+    attn_us = attn_timer.durations_us()
+    attn_mean = sum(attn_us) / len(attn_us)
+    attn_bytes = (total * wl.num_kv_heads * wl.head_dim * 2 * q.element_size()
+                  + 2 * q.numel() * q.element_size())
+    log(f"[bench] {args.steps} store+attention steps: {attn_step_ms:.3f} ms/step, "
+        f"attention {attn_mean:.1f} us/layer")
 
     store_bytes = wl.store_bytes()
     gather_bytes = wl.gather_bytes()
@@ -203,7 +209,34 @@ def main(argv=None) -> int:
 
     cpu_baseline = None
     if not args.profile and args.cpu_baseline_layers > 0:
-        cpu_baseline = run_cpu_baseline(wl, args.cpu_baseline_layers, args.cpu_baseline_repeats)
+        check_layers = [int(x) for x in args.check_layers.split(",") if x.strip()]
+
+        def gpu_layer(layer: int) -> dict:
+            """Host copies of the GPU store+gather and attention outputs of
+            one layer for the packed step, and the layer's cache before the
+            store (the store is idempotent: the timed steps stored the same
+            rows, so the oracle replaying it on this copy is exact)."""
+            tables = wl.padded_block_tables()
+            used = np.unique(tables[tables >= 0])
+            index = torch.from_numpy(used.astype(np.int64)).to(device)
+            kc, vc = cache[0, layer], cache[1, layer]
+            before = [c.index_select(0, index).cpu().view(torch.int16).numpy() for c in (kc, vc)]
+            ctx = packer.pack_decode(batch)
+            plan = backend.build_gather_plan(kc, ctx.block_tables, ctx.cu_seqlens_k, total)
+            backend.store(new_k[layer], new_v[layer], kc, vc, ctx.slot_mapping)
+            backend.gather_varlen(kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
+                                  plan=plan, out=(k_out, v_out))
+            backend.paged_attention_decode(q, kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
+                                           softmax_scale, out=attn_out)
+            torch.cuda.synchronize()
+            return {"used_blocks": used, "before": before,
+                    "k_out": k_out.cpu().view(torch.int16).numpy(),
+                    "v_out": v_out.cpu().view(torch.int16).numpy(),
+                    "attention": attn_out.float().cpu().numpy(),
+                    "q": q.float().cpu().numpy(), "scale": softmax_scale}
+
+        cpu_baseline = cpu_baseline_leg(wl, args.cpu_baseline_layers, args.cpu_baseline_repeats,
+                                        check_layers, gpu_layer)
 
     result = {
         "metric": METRIC,
@@ -252,12 +285,68 @@ def main(argv=None) -> int:
             "traffic_source": "profiles/gather_varlen_decode_step_traffic.json" if traffic else None,
             "algorithmic_bytes_per_launch": gather_launch_bytes,
         },
+        "attention": {
+            "kernel": "paged_attention_decode (split-K partials + merge, one layer, 16 q heads "
+                      "over 8 kv heads, straight from the paged cache)",
+            "us": summarize_latencies(attn_us),
+            "achieved": round(attn_bytes / (attn_mean * 1e-6) / 1e9, 2),
+            "peak": MI355X_HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(attn_bytes / (attn_mean * 1e-6) / 1e9 / MI355X_HBM_PEAK_GBPS, 4),
+            "algorithmic_bytes_per_launch": attn_bytes,
+            "step_ms_store_attention": round(attn_step_ms, 4),
+            "decode_tokens_per_s_store_attention": round(B / (attn_step_ms * 1e-3), 2),
+        },
         "cpu_baseline": cpu_baseline,
         "host": {"platform": platform.platform(), "torch": torch.__version__, "hip": torch.version.hip,
                  "gpu": torch.cuda.get_device_name(device)},
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer) -> dict:
+    """The CPU leg: the oracle checks the GPU's outputs of ``check_layers``
+    (store+gather bit-exact; attention within 1e-3 + 1e-2*|ref| of the fp32
+    oracle on 32 sequences), then its C restatement is timed on the host
+    cores (:func:`run_cpu_baseline`)."""
+    import numpy as np
+    import torch
+
+    from oracle import c_oracle
+    from oracle import paged_kv as oracle
+
+    threads = c_oracle.default_threads()
+    tables = wl.padded_block_tables()
+    cu = wl.cu_seqlens_k()
+    checked = []
+    for layer in check_layers:
+        got = gpu_layer(layer)
+        used = got["used_blocks"]
+        remap = np.full(wl.num_blocks, -1, np.int64)
+        remap[used] = np.arange(used.size)
+        ctables = np.where(tables >= 0, remap[np.maximum(tables, 0)], -1).astype(np.int32)
+        cslots = (remap[wl.slot_mapping // wl.block_size] * wl.block_size
+                  + wl.slot_mapping % wl.block_size).astype(np.int32)
+        hk, hv = got["before"]
+        c_oracle.store(wl.key[layer].view(torch.int16).numpy(), wl.value[layer].view(torch.int16).numpy(),
+                       hk, hv, cslots, threads=threads)
+        for name, host in (("k_out", hk), ("v_out", hv)):
+            expected = c_oracle.gather_varlen(host, ctables, cu, threads=threads)
+            if not np.array_equal(got[name], expected):
+                raise AssertionError(f"decode step layer {layer}: gather differs from the oracle")
+        sample = np.linspace(0, wl.num_seqs - 1, 32).astype(np.int64)
+        ref = oracle.paged_attention_decode(got["q"][sample], hk, hv, ctables[sample],
+                                            wl.num_tokens[sample], got["scale"])
+        err = np.abs(got["attention"][sample] - ref)
+        if (err > 1e-3 + 1e-2 * np.abs(ref)).any():
+            raise AssertionError(f"decode step layer {layer}: attention differs from the oracle "
+                                 f"(max err {err.max():.3e})")
+        log(f"[bench] layer {layer}: store+gather bit-exact, attention max err {err.max():.2e} vs oracle")
+        checked.append(layer)
+    result = run_cpu_baseline(wl, layers, repeats)
+    result["checked_layers"] = checked
+    return result
 
 
 def run_cpu_baseline(wl, layers: int, repeats: int) -> dict:
