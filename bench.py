@@ -36,6 +36,23 @@ for _p in (REPO_ROOT, REPO_ROOT / "nano-vllm-multimodal_amd"):
 
 METRIC = "paged KV store+gather GB/s (fraction of HBM peak); decode-step tokens/s, 1 GPU"
 TRAFFIC_FILE = REPO_ROOT / "profiles" / "gather_varlen_decode_step_traffic.json"
+ATTENTION_TRAFFIC_FILE = REPO_ROOT / "profiles" / "paged_attention_decode_step_traffic.json"
+
+
+def measured_traffic(path: Path, algorithmic_bytes: int):
+    """HBM bytes per launch from a committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a copy of known size), or None
+    unless it was measured on this workload (same algorithmic bytes)."""
+    if not path.is_file():
+        return None
+    try:
+        t = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    if (t.get("workload") == "decode_step" and t.get("layers_per_launch") == 1
+            and t.get("algorithmic_bytes_per_launch") == algorithmic_bytes):
+        return t.get("bytes_per_launch")
+    return None
 
 
 def parse_args(argv=None):
@@ -194,18 +211,8 @@ def main(argv=None) -> int:
     gather_mean = sum(gather_us) / len(gather_us)
     achieved = gather_launch_bytes / (gather_mean * 1e-6) / 1e9
 
-    # HBM bytes per gather launch, from the committed rocprofv3 FETCH_SIZE /
-    # WRITE_SIZE passes (calibrated against a copy of known size); valid only
-    # for this workload, whose algorithmic bytes it was measured against.
-    traffic = None
-    if TRAFFIC_FILE.is_file():
-        try:
-            t = json.loads(TRAFFIC_FILE.read_text())
-            if (t.get("workload") == "decode_step" and t.get("layers_per_launch") == 1
-                    and t.get("algorithmic_bytes_per_launch") == wl.gather_bytes(layers=1)):
-                traffic = t.get("bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    traffic = measured_traffic(TRAFFIC_FILE, wl.gather_bytes(layers=1))
+    attn_traffic = measured_traffic(ATTENTION_TRAFFIC_FILE, attn_bytes)
 
     cpu_baseline = None
     if not args.profile and args.cpu_baseline_layers > 0:
@@ -294,6 +301,9 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(attn_bytes / (attn_mean * 1e-6) / 1e9 / MI355X_HBM_PEAK_GBPS, 4),
             "algorithmic_bytes_per_launch": attn_bytes,
+            "traffic": attn_traffic,
+            "traffic_source": ("profiles/paged_attention_decode_step_traffic.json"
+                               if attn_traffic else None),
             "step_ms_store_attention": round(attn_step_ms, 4),
             "decode_tokens_per_s_store_attention": round(B / (attn_step_ms * 1e-3), 2),
         },
