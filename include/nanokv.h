@@ -310,6 +310,110 @@ int nkv_transfer_poll(nkv_transfer* lane, int64_t* in_flight,
                       int64_t* completed_upto);
 int nkv_transfer_synchronize(nkv_transfer* lane);
 
+/*
+ * Device block pool: the block bookkeeping of the reference BlockManager,
+ * resident in HBM.
+ *   - the free-block FIFO: fresh blocks from the front, freed blocks to the
+ *     back, a prefix hit on a free block leaving the queue where it stands;
+ *   - the reference counts;
+ *   - one block table per sequence slot.
+ *
+ * Replaces: BlockManager._allocate_block / _deallocate_block / allocate /
+ *   deallocate / may_append (nanovllm/engine/block_manager.py:87-118,
+ *   185-236), and the upload of every sequence's block list that
+ *   ModelRunner.prepare_block_tables feeds on (model_runner.py:696-707).
+ *   The prefix-hash chain (compute_hash, hash_to_block_id, hash_blocks,
+ *   :65-85, 229-258) stays with the caller, which passes each allocation's
+ *   cached-prefix block ids.
+ *
+ * The state lives in one device buffer the caller owns (the library never
+ *   allocates): nkv_pool_bytes gives its size, nkv_pool_offsets the byte
+ *   offsets of its arrays (META, RING, QPOS, REF, TABLES, NBLK), and an
+ *   nkv_pool_desc names the buffer (256-byte aligned) and its geometry.
+ * nkv_pool_init initialises the state on `stream`: every block free in id
+ *   order, every table empty, no error.
+ * nkv_pool_apply runs an op log (device memory, int32) in order on one
+ *   workgroup:
+ *     ops  [num_ops][4] {type, slot, num_blocks, args_offset}, 16-B aligned;
+ *     args for ALLOCATE: args[args_offset] = number of cached-prefix ids k,
+ *          then the k ids (distinct; each either used, gaining a reference,
+ *          or free, leaving the queue).
+ *     ALLOCATE   slot takes num_blocks blocks: the k cached ids, then
+ *                num_blocks - k blocks from the queue front (slot must hold
+ *                no blocks; num_blocks <= max_blocks_per_seq);
+ *     DEALLOCATE slot releases its blocks in reversed table order; a block
+ *                whose count reaches zero goes to the back of the queue;
+ *     APPEND     slot takes one block from the queue front (the reference
+ *                calls may_append when len(seq) % block_size == 1); a run of
+ *                consecutive APPENDs must name distinct slots;
+ *     FENCE      no-op (ends an APPEND run).
+ *   Every op is validated before it changes anything.  The first invalid op
+ *   (bad slot or block, table busy/full, not enough free blocks) is recorded
+ *   in meta[3] (its index + 1) and meta[4] (an NKV_POOL_ERR_* code) and
+ *   ends the log; later logs are ignored until nkv_pool_init.
+ * The arrays (at nkv_pool_offsets[k], in the order of the NKV_POOL_* ids):
+ *     META   int64[8] = head, tail, live free blocks, error op + 1, error
+ *            code;
+ *     RING   int32[2*num_blocks], the queue, -1 tombstones;
+ *     QPOS   int64[num_blocks];
+ *     REF    int32[num_blocks];
+ *     TABLES int32[max_seqs * max_blocks_per_seq], -1 padded;
+ *     NBLK   int32[max_seqs].
+ *   Free blocks in order are the non-negative RING entries of absolute
+ *   positions [head, tail), ring index = position % (2*num_blocks).
+ * nkv_pack_decode_pool / nkv_pack_prefill_pool are nkv_pack_decode /
+ *   nkv_pack_prefill with sequence i's block list read from the pool's
+ *   table of slot seq_slots[i] instead of a host-built CSR.
+ */
+typedef struct nkv_pool_desc {
+  void* memory;               /* nkv_pool_bytes(...) bytes of device memory */
+  int64_t num_blocks;
+  int64_t max_seqs;           /* sequence slots */
+  int64_t max_blocks_per_seq; /* table width */
+} nkv_pool_desc;
+#define NKV_POOL_OP_ALLOCATE 1
+#define NKV_POOL_OP_DEALLOCATE 2
+#define NKV_POOL_OP_APPEND 3
+#define NKV_POOL_OP_FENCE 4
+#define NKV_POOL_META 0
+#define NKV_POOL_RING 1
+#define NKV_POOL_QPOS 2
+#define NKV_POOL_REF 3
+#define NKV_POOL_TABLES 4
+#define NKV_POOL_NBLK 5
+#define NKV_POOL_ERR_BAD_OP 1        /* unknown op type                  */
+#define NKV_POOL_ERR_BAD_SLOT 2      /* slot outside [0, max_seqs)       */
+#define NKV_POOL_ERR_TABLE_BUSY 3    /* ALLOCATE on a slot holding blocks */
+#define NKV_POOL_ERR_TABLE_FULL 4    /* APPEND past max_blocks_per_seq   */
+#define NKV_POOL_ERR_NO_FREE 5       /* not enough free blocks           */
+#define NKV_POOL_ERR_BAD_BLOCK 6     /* block id out of range / unowned  */
+#define NKV_POOL_ERR_BAD_ARGS 7      /* counts or args offset invalid    */
+#define NKV_POOL_MAX_BLOCKS (1 << 28)
+#define NKV_POOL_MAX_SEQS 65536
+int64_t nkv_pool_bytes(int64_t num_blocks, int64_t max_seqs,
+                       int64_t max_blocks_per_seq);
+int nkv_pool_offsets(int64_t num_blocks, int64_t max_seqs,
+                     int64_t max_blocks_per_seq, int64_t* offsets /* [6] */);
+int nkv_pool_init(const nkv_pool_desc* pool, void* stream);
+int nkv_pool_apply(const nkv_pool_desc* pool, const int32_t* ops, int64_t num_ops,
+                   const int32_t* args, int64_t num_args, void* stream);
+int nkv_pack_decode_pool(const nkv_pool_desc* pool, const int32_t* num_tokens,
+                         const int32_t* seq_slots, int64_t num_seqs,
+                         int64_t padded_seqs, int64_t block_size,
+                         int64_t table_width, int64_t table_stride,
+                         int32_t* slot_mapping, int32_t* context_lens,
+                         int32_t* block_tables, int32_t* cu_seqlens_k,
+                         void* stream);
+int nkv_pack_prefill_pool(const nkv_pool_desc* pool, const int32_t* num_cached,
+                          const int32_t* num_scheduled, const int32_t* num_prompt,
+                          const int32_t* seq_slots, int64_t num_seqs,
+                          int64_t block_size, int64_t table_width,
+                          int64_t num_slots, int32_t* cu_seqlens_q,
+                          int32_t* cu_seqlens_k, int32_t* slot_mapping,
+                          int32_t* block_tables, int32_t* full_context_lens,
+                          int32_t* query_start_lens, int32_t* max_seqlens,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

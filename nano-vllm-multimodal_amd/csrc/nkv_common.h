@@ -168,6 +168,12 @@ int launch_block_plan(const int32_t* tables, int64_t table_stride,
                       int32_t* first_chunk, hipStream_t stream,
                       const char* what);
 
+// Validates a block-pool descriptor and returns the device addresses of its
+// block tables [max_seqs, max_blocks_per_seq] and counts [max_seqs]
+// (defined in nkv_pool.hip).
+int pool_tables(const nkv_pool_desc* pool, const char* what, const int32_t** tables,
+                const int32_t** nblk);
+
 }  // namespace nkv
 
 // Error reporting shared by all translation units (defined in nkv_api.hip).

@@ -20,6 +20,21 @@ c_ptr = ctypes.c_void_p
 c_ptr_out = ctypes.POINTER(ctypes.c_void_p)
 c_i64_out = ctypes.POINTER(ctypes.c_int64)
 
+
+class PoolDesc(ctypes.Structure):
+    """struct nkv_pool_desc: the device buffer holding a block pool and its
+    geometry."""
+
+    _fields_ = [
+        ("memory", ctypes.c_void_p),
+        ("num_blocks", ctypes.c_int64),
+        ("max_seqs", ctypes.c_int64),
+        ("max_blocks_per_seq", ctypes.c_int64),
+    ]
+
+
+c_pool = ctypes.POINTER(PoolDesc)
+
 # name -> (restype, argtypes); mirrors include/nanokv.h.
 SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     "nkv_version": (ctypes.c_int, ()),
@@ -80,6 +95,34 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     "nkv_transfer_h2d": (ctypes.c_int, (c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64_out)),
     "nkv_transfer_poll": (ctypes.c_int, (c_ptr, c_i64_out, c_i64_out)),
     "nkv_transfer_synchronize": (ctypes.c_int, (c_ptr,)),
+    "nkv_pool_bytes": (c_i64, (c_i64, c_i64, c_i64)),
+    "nkv_pool_offsets": (ctypes.c_int, (c_i64, c_i64, c_i64, c_i64_out)),
+    "nkv_pool_init": (ctypes.c_int, (c_pool, c_ptr)),
+    "nkv_pool_apply": (ctypes.c_int, (c_pool, c_ptr, c_i64, c_ptr, c_i64, c_ptr)),
+    "nkv_pack_decode_pool": (
+        ctypes.c_int,
+        (c_pool, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_ptr),
+    ),
+    "nkv_pack_prefill_pool": (
+        ctypes.c_int,
+        (c_pool, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr,
+         c_ptr, c_ptr, c_ptr, c_ptr, c_ptr),
+    ),
+}
+
+NKV_POOL_OP_ALLOCATE = 1
+NKV_POOL_OP_DEALLOCATE = 2
+NKV_POOL_OP_APPEND = 3
+NKV_POOL_OP_FENCE = 4
+NKV_POOL_ERRORS = {
+    1: "unknown op type",
+    2: "slot outside [0, max_seqs)",
+    3: "allocate on a slot that holds blocks",
+    4: "append past max_blocks_per_seq",
+    5: "not enough free blocks",
+    6: "block id out of range or not owned",
+    7: "bad counts or args offset",
 }
 
 NKV_DTYPE_FLOAT16 = 0

@@ -16,6 +16,7 @@ The result is a :class:`Context` with the fields of the reference's
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Iterable, Sequence
 
@@ -317,6 +318,115 @@ class DevicePacker:
             context_lens=buffers.context_lens[:b],
             block_tables=buffers.block_tables[:b],
             total_context_tokens=int(batch.num_tokens.astype(np.int64).sum()),
+        )
+
+    def pack_decode_pool(self, pool, seq_slots, num_tokens, *,
+                         table_width: int | None = None) -> Context:
+        """pack_decode with each sequence's block list read from the device
+        block pool (table of slot seq_slots[i]) instead of an uploaded CSR:
+        only the slots and token counts travel.  The tables are padded to
+        the longest list, ceil(num_tokens / block_size) blocks, as
+        prepare_block_tables pads (model_runner.py:696-707)."""
+        slots_h = _int32_array(seq_slots, "seq_slots")
+        tokens_h = _int32_array(num_tokens, "num_tokens")
+        b = int(slots_h.size)
+        if tokens_h.size != b:
+            raise ValueError("seq_slots and num_tokens must have one entry per sequence")
+        if b > _lib.NKV_MAX_PACK_SEQS:
+            raise ValueError(f"device packing supports at most {_lib.NKV_MAX_PACK_SEQS} sequences per step")
+        if b and bool((tokens_h < 1).any()):
+            raise ValueError("every decoding sequence needs at least one token")
+        if b and (bool((slots_h < 0).any()) or bool((slots_h >= pool.max_seqs).any())):
+            raise ValueError("seq_slots must name slots of the pool")
+        if pool.block_size != self.block_size or pool.device != self.device:
+            raise ValueError("the pool has another block size or device")
+        longest = int(((tokens_h.astype(np.int64) + self.block_size - 1) // self.block_size).max()) if b else 0
+        width = longest if table_width is None else int(table_width)
+        if width < longest or width > pool.width:
+            raise ValueError("table_width must cover the longest block list and fit the pool")
+        d_tokens, d_slots = self._upload([tokens_h, slots_h])
+        out = torch.empty(3 * b + 1 + b * width, dtype=torch.int32, device=self.device)
+        slots = out[:b]
+        context_lens = out[b: 2 * b]
+        cu_seqlens_k = out[2 * b: 3 * b + 1]
+        tables = out[3 * b + 1:].view(b, width)
+        status = _lib.load_library().nkv_pack_decode_pool(
+            ctypes.byref(pool.desc), d_tokens.data_ptr(), d_slots.data_ptr(), b, b, self.block_size,
+            width, width, slots.data_ptr(), context_lens.data_ptr(),
+            tables.data_ptr() if tables.numel() else None, cu_seqlens_k.data_ptr(), self._stream(),
+        )
+        _lib.check(status, "nkv_pack_decode_pool")
+        return Context(
+            is_prefill=False,
+            cu_seqlens_k=cu_seqlens_k,
+            max_seqlen_k=int(tokens_h.max()) if b else 0,
+            slot_mapping=slots,
+            context_lens=context_lens,
+            block_tables=tables,
+            total_context_tokens=int(tokens_h.astype(np.int64).sum()),
+        )
+
+    def pack_prefill_pool(self, pool, seq_slots, num_cached_tokens, num_scheduled_tokens,
+                          num_prompt_tokens=None, *, table_width: int | None = None,
+                          force_block_tables: bool = False) -> Context:
+        """pack_prefill with each sequence's block list read from the device
+        block pool.  A sequence's list covers its whole prompt (allocate
+        takes ceil(len / block_size) blocks), so the host checks coverage
+        from the token counts; the tables are padded to the longest list."""
+        slots_h = _int32_array(seq_slots, "seq_slots")
+        cached_h = _int32_array(num_cached_tokens, "num_cached_tokens")
+        sched_h = _int32_array(num_scheduled_tokens, "num_scheduled_tokens")
+        b = int(slots_h.size)
+        if cached_h.size != b or sched_h.size != b:
+            raise ValueError("one entry per sequence in every array")
+        if b > _lib.NKV_MAX_PACK_SEQS:
+            raise ValueError(f"device packing supports at most {_lib.NKV_MAX_PACK_SEQS} sequences per step")
+        if b and (bool((cached_h < 0).any()) or bool((sched_h < 0).any())):
+            raise ValueError("cached and scheduled token counts must be non-negative")
+        if b and (bool((slots_h < 0).any()) or bool((slots_h >= pool.max_seqs).any())):
+            raise ValueError("seq_slots must name slots of the pool")
+        if pool.block_size != self.block_size or pool.device != self.device:
+            raise ValueError("the pool has another block size or device")
+        ends = cached_h.astype(np.int64) + sched_h
+        prompt_h = (_int32_array(num_prompt_tokens, "num_prompt_tokens")
+                    if num_prompt_tokens is not None else ends.astype(np.int32))
+        if prompt_h.size != b:
+            raise ValueError("one entry per sequence in every array")
+        blocks = (np.maximum(prompt_h.astype(np.int64), ends) + self.block_size - 1) // self.block_size
+        num_slots = int(sched_h.astype(np.int64).sum())
+        with_tables = force_block_tables or int(cached_h.astype(np.int64).sum()) > 0
+        longest = int(blocks.max()) if b else 0
+        width = (longest if table_width is None else int(table_width)) if with_tables else 0
+        if with_tables and (width < longest or width > pool.width):
+            raise ValueError("table_width must cover the longest block list and fit the pool")
+        d_cached, d_sched, d_prompt, d_slots = self._upload([cached_h, sched_h, prompt_h, slots_h])
+        sizes = [b + 1, b + 1, num_slots, b * width, b, b, 2]
+        out = torch.empty(sum(sizes), dtype=torch.int32, device=self.device)
+        views, offset = [], 0
+        for size in sizes:
+            views.append(out[offset: offset + size])
+            offset += size
+        cu_q, cu_k, slots, tables, full_ctx, q_start, max_lens = views
+        tables = tables.view(b, width) if with_tables else None
+        status = _lib.load_library().nkv_pack_prefill_pool(
+            ctypes.byref(pool.desc), d_cached.data_ptr(), d_sched.data_ptr(), d_prompt.data_ptr(),
+            d_slots.data_ptr(), b, self.block_size, width, num_slots, cu_q.data_ptr(),
+            cu_k.data_ptr(), slots.data_ptr() if num_slots else None,
+            tables.data_ptr() if tables is not None and tables.numel() else None,
+            full_ctx.data_ptr(), q_start.data_ptr(), max_lens.data_ptr(), self._stream(),
+        )
+        _lib.check(status, "nkv_pack_prefill_pool")
+        return Context(
+            is_prefill=True,
+            cu_seqlens_q=cu_q,
+            cu_seqlens_k=cu_k,
+            max_seqlen_q=int(sched_h.max()) if b else 0,
+            max_seqlen_k=int(ends.max()) if b else 0,
+            slot_mapping=slots,
+            block_tables=tables,
+            full_context_lens=full_ctx,
+            query_start_lens=q_start,
+            total_context_tokens=int(ends.sum()),
         )
 
     # ------------------------------------------------------------ prefill
