@@ -211,6 +211,10 @@ def main(argv=None) -> int:
     gather_mean = sum(gather_us) / len(gather_us)
     achieved = gather_launch_bytes / (gather_mean * 1e-6) / 1e9
 
+    block_pool = measure_block_pool(wl, device, packer, batch, args.steps, args.warmup)
+    log(f"[bench] block pool: {block_pool['gpu_us_per_step']:.1f} us GPU, "
+        f"{block_pool['host_us_per_step']:.1f} us host per step")
+
     traffic = measured_traffic(TRAFFIC_FILE, wl.gather_bytes(layers=1))
     attn_traffic = measured_traffic(ATTENTION_TRAFFIC_FILE, attn_bytes)
 
@@ -307,12 +311,121 @@ def main(argv=None) -> int:
             "step_ms_store_attention": round(attn_step_ms, 4),
             "decode_tokens_per_s_store_attention": round(B / (attn_step_ms * 1e-3), 2),
         },
+        "block_pool": block_pool,
         "cpu_baseline": cpu_baseline,
         "host": {"platform": platform.platform(), "torch": torch.__version__, "hip": torch.version.hip,
                  "gpu": torch.cuda.get_device_name(device)},
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+def block_pool_steps(wl, seed: int = 11):
+    """The decode step's block bookkeeping as an endless run of scheduler
+    steps: the 256 running sequences each grow by one token (a new block
+    when the token opens one), then 16 finish and 16 are admitted with
+    contexts from the same law.  Yields, per step, the op list and the
+    running (slot, tokens) pairs; block accounting is exact on the host
+    because no block is shared."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    bs = wl.block_size
+    lens = {slot: int(n) for slot, n in enumerate(wl.num_tokens)}
+    free_slots = list(range(wl.num_seqs, 2 * wl.num_seqs))
+    held = {slot: -(-n // bs) for slot, n in lens.items()}
+    free_blocks = wl.num_blocks - sum(held.values())
+    yield [("allocate", slot, held[slot]) for slot in lens], dict(lens)
+    while True:
+        ops = []
+        for slot in list(lens):
+            if lens[slot] % bs == 0:
+                if free_blocks == 0:  # can_append fails: the sequence waits
+                    continue
+                ops.append(("append", slot))
+                held[slot] += 1
+                free_blocks -= 1
+            lens[slot] += 1
+        for slot in rng.choice(sorted(lens), 16, replace=False).tolist():
+            ops.append(("deallocate", slot))
+            free_blocks += held.pop(slot)
+            del lens[slot]
+            free_slots.append(slot)
+        contexts = np.floor(np.exp(np.log(256) + rng.random(16) * (np.log(16384) - np.log(256))))
+        for n_tokens in contexts.astype(np.int64).tolist():
+            n = -(-int(n_tokens) // bs)
+            if n > free_blocks or not free_slots:
+                continue
+            slot = free_slots.pop(0)
+            ops.append(("allocate", slot, n))
+            held[slot] = n
+            free_blocks -= n
+            lens[slot] = int(n_tokens)
+        yield ops, dict(lens)
+
+
+def measure_block_pool(wl, device, packer, batch, steps: int, warmup: int) -> dict:
+    """Per decode step: record the step's BlockManager calls, replay them
+    on the device pool and pack the step from the pool's tables, against
+    packing the same batch shape from an uploaded CSR (the path without
+    the pool).  GPU time from events on the current stream; host time is
+    the Python recording + launch cost."""
+    import numpy as np
+    import torch
+
+    from nanokv.benchmark import LaunchTimer
+    from nanokv.pool import DeviceBlockPool
+
+    width = -(-(16384 + 4 * (steps + warmup) + 1) // wl.block_size) + 1
+    pool = DeviceBlockPool(wl.num_blocks, wl.block_size, max_seqs=2 * wl.num_seqs,
+                           max_blocks_per_seq=width, device=device)
+    stream = torch.cuda.current_stream(device)
+    gen = block_pool_steps(wl)
+    pool_timer, csr_timer = LaunchTimer(stream), LaunchTimer(stream)
+    host_s, log_bytes = [], []
+
+    def run(ops, lens, timed: bool):
+        t0 = time.perf_counter()
+        e0 = pool_timer.start() if timed else None
+        for op in ops:
+            if op[0] == "append":
+                pool.append(op[1])
+            elif op[0] == "deallocate":
+                pool.deallocate(op[1])
+            else:
+                pool.allocate(op[1], op[2])
+        n_ops, n_args = pool.pending_ops, len(pool._args)
+        pool.flush()
+        slots = sorted(lens)
+        packer.pack_decode_pool(pool, slots, [lens[s] for s in slots])
+        if timed:
+            pool_timer.stop(e0)
+            host_s.append(time.perf_counter() - t0)
+            log_bytes.append(16 * n_ops + 4 * n_args + 8 * len(slots))
+            e1 = csr_timer.start()
+            packer.pack_decode(batch)
+            csr_timer.stop(e1)
+
+    ops, lens = next(gen)
+    run(ops, lens, False)
+    for _ in range(warmup):
+        run(*next(gen), False)
+    for _ in range(steps):
+        run(*next(gen), True)
+    torch.cuda.synchronize()
+    pool.check()
+    pool_us = pool_timer.durations_us()
+    csr_us = csr_timer.durations_us()
+    csr_bytes = 4 * (2 * batch.num_seqs + 1 + int(batch.block_ids.size))
+    return {
+        "step": "256 running sequences +1 token (append when a block opens), 16 finish, "
+                "16 admitted; replay on the device pool, then pack_decode_pool",
+        "gpu_us_per_step": round(float(np.mean(pool_us)), 2),
+        "host_us_per_step": round(1e6 * float(np.mean(host_s)), 2),
+        "upload_bytes_per_step": int(np.mean(log_bytes)),
+        "csr_pack_gpu_us_per_step": round(float(np.mean(csr_us)), 2),
+        "csr_upload_bytes_per_step": csr_bytes,
+    }
 
 
 def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer) -> dict:
@@ -356,6 +469,28 @@ def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer) -> 
         checked.append(layer)
     result = run_cpu_baseline(wl, layers, repeats)
     result["checked_layers"] = checked
+
+    # The block bookkeeping of the same decode steps on the host: the
+    # oracle's restatement of BlockManager, one Python call per op as the
+    # reference makes them.
+    from oracle.block_pool import BlockPoolOracle
+
+    book = BlockPoolOracle(wl.num_blocks)
+    gen = block_pool_steps(wl)
+    step_s = []
+    for k in range(1 + 50):
+        ops, _ = next(gen)
+        t0 = time.perf_counter()
+        for op in ops:
+            if op[0] == "append":
+                book.append(op[1])
+            elif op[0] == "deallocate":
+                book.deallocate(op[1])
+            else:
+                book.allocate(op[1], op[2])
+        if k:
+            step_s.append(time.perf_counter() - t0)
+    result["block_pool_python_us_per_step"] = round(1e6 * sum(step_s) / len(step_s), 2)
     return result
 
 

@@ -344,9 +344,11 @@ int nkv_transfer_synchronize(nkv_transfer* lane);
  *     DEALLOCATE slot releases its blocks in reversed table order; a block
  *                whose count reaches zero goes to the back of the queue;
  *     APPEND     slot takes one block from the queue front (the reference
- *                calls may_append when len(seq) % block_size == 1); a run of
- *                consecutive APPENDs must name distinct slots;
- *     FENCE      no-op (ends an APPEND run).
+ *                calls may_append when len(seq) % block_size == 1);
+ *     FENCE      no-op.
+ *   Consecutive APPENDs, and consecutive ALLOCATEs without cached ids, run
+ *   as one parallel step up to the first repeated slot; the result is the
+ *   one-op-at-a-time result.
  *   Every op is validated before it changes anything.  The first invalid op
  *   (bad slot or block, table busy/full, not enough free blocks) is recorded
  *   in meta[3] (its index + 1) and meta[4] (an NKV_POOL_ERR_* code) and

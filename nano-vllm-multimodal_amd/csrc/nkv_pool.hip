@@ -25,10 +25,11 @@
 // One workgroup of 1024 threads applies the whole log: ops are sequential
 // (each depends on the queue the previous one left), the work inside an op
 // is parallel (block-wide scans order the pops and pushes), and a run of
-// consecutive appends is one parallel pop.  Every op is validated before it
-// changes anything; the first invalid op is recorded in meta and ends the
-// log, so the state is always the reference's state after the valid prefix
-// of the log.
+// appends, or of allocations without cached ids, to distinct slots is one
+// parallel pop in op order.  Every op is validated before it changes
+// anything; the first invalid op is recorded in meta and ends the log, so
+// the state is always the reference's state after the valid prefix of the
+// log.
 #include "nkv_common.h"
 
 namespace nkv {
@@ -44,6 +45,7 @@ struct PoolView {
   int32_t* ref;
   int32_t* tables;
   int32_t* nblk;
+  int32_t* slot_mark;  // scratch, zero between launches
   int32_t num_blocks;
   int32_t max_seqs;
   int32_t width;
@@ -52,16 +54,17 @@ struct PoolView {
 
 int64_t align256(int64_t n) { return (n + 255) & ~int64_t{255}; }
 
-// Byte offsets of META, RING, QPOS, REF, TABLES, NBLK and the total size.
-void pool_layout(int64_t num_blocks, int64_t max_seqs, int64_t width, int64_t offsets[7]) {
-  const int64_t sizes[6] = {kMetaWords * 8, 2 * num_blocks * 4, num_blocks * 8, num_blocks * 4,
-                            max_seqs * width * 4, max_seqs * 4};
+// Byte offsets of META, RING, QPOS, REF, TABLES, NBLK, the slot-mark
+// scratch (int32[max_seqs], zero between launches) and the total size.
+void pool_layout(int64_t num_blocks, int64_t max_seqs, int64_t width, int64_t offsets[8]) {
+  const int64_t sizes[7] = {kMetaWords * 8, 2 * num_blocks * 4, num_blocks * 8, num_blocks * 4,
+                            max_seqs * width * 4, max_seqs * 4, max_seqs * 4};
   int64_t at = 0;
-  for (int k = 0; k < 6; ++k) {
+  for (int k = 0; k < 7; ++k) {
     offsets[k] = at;
     at += align256(sizes[k]);
   }
-  offsets[6] = at;
+  offsets[7] = at;
 }
 
 bool geometry_ok(int64_t num_blocks, int64_t max_seqs, int64_t width) {
@@ -71,12 +74,13 @@ bool geometry_ok(int64_t num_blocks, int64_t max_seqs, int64_t width) {
 }
 
 PoolView view_of(const nkv_pool_desc& d) {
-  int64_t off[7];
+  int64_t off[8];
   pool_layout(d.num_blocks, d.max_seqs, d.max_blocks_per_seq, off);
   auto* base = static_cast<uint8_t*>(d.memory);
   return PoolView{reinterpret_cast<int64_t*>(base + off[0]), reinterpret_cast<int32_t*>(base + off[1]),
                   reinterpret_cast<int64_t*>(base + off[2]), reinterpret_cast<int32_t*>(base + off[3]),
                   reinterpret_cast<int32_t*>(base + off[4]), reinterpret_cast<int32_t*>(base + off[5]),
+                  reinterpret_cast<int32_t*>(base + off[6]),
                   static_cast<int32_t>(d.num_blocks), static_cast<int32_t>(d.max_seqs),
                   static_cast<int32_t>(d.max_blocks_per_seq), 2 * d.num_blocks};
 }
@@ -93,7 +97,10 @@ __global__ void pool_init_kernel(PoolView v) {
   }
   const int64_t cells = static_cast<int64_t>(v.max_seqs) * v.width;
   for (int64_t i = start; i < cells; i += stride) v.tables[i] = -1;
-  for (int64_t i = start; i < v.max_seqs; i += stride) v.nblk[i] = 0;
+  for (int64_t i = start; i < v.max_seqs; i += stride) {
+    v.nblk[i] = 0;
+    v.slot_mark[i] = 0;
+  }
   if (start == 0) {
     v.meta[0] = 0;             // head
     v.meta[1] = v.num_blocks;  // tail
@@ -180,14 +187,53 @@ enum : int32_t {
   kErrBadArgs = NKV_POOL_ERR_BAD_ARGS,
 };
 
+// The run of ops starting at i that `qualifies` (at most kPoolThreads of
+// them), cut before the first op whose slot already appeared in the run, so
+// the run's ops touch distinct tables and can proceed in parallel.  Slot
+// marks (zero between launches) find the first occurrence of each slot:
+// every op raises its slot's mark to kPoolThreads - k, so the mark names
+// the smallest k.  Thread k returns ops[i + k] in *mine.
+template <typename Qualifies>
+__device__ int32_t run_length(const PoolView& v, const int4* __restrict__ ops, int64_t i,
+                              int64_t num_ops, Qualifies qualifies, int32_t* s_end,
+                              int4* mine) {
+  const int32_t t = threadIdx.x;
+  const int32_t n = static_cast<int32_t>(min<int64_t>(kPoolThreads, num_ops - i));
+  if (t == 0) *s_end = n;
+  __syncthreads();
+  int4 op = make_int4(0, -1, 0, 0);
+  if (t < n) {
+    op = ops[i + t];
+    if (!qualifies(op)) atomicMin(s_end, t);
+  }
+  *mine = op;
+  __syncthreads();
+  const int32_t end = *s_end;
+  const bool marked = t < end && op.y >= 0 && op.y < v.max_seqs;
+  if (marked) atomicMax(&v.slot_mark[op.y], kPoolThreads - t);
+  __syncthreads();
+  if (marked && __hip_atomic_load(&v.slot_mark[op.y], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) != kPoolThreads - t) {
+    atomicMin(s_end, t);  // a repeat: the run stops before it
+  }
+  __syncthreads();
+  if (marked) v.slot_mark[op.y] = 0;
+  const int32_t cut = *s_end;
+  __syncthreads();
+  return cut;
+}
+
 // ops: int4 per op {type, slot, num_blocks (allocate), args offset
 // (allocate)}; args[off] = number of cached ids, args[off+1 ...] the ids.
 __global__ __launch_bounds__(kPoolThreads) void pool_apply_kernel(
     PoolView v, const int4* __restrict__ ops, int64_t num_ops,
     const int32_t* __restrict__ args, int64_t num_args) {
   __shared__ int32_t s_tmp[kPoolThreads / kWave + 1];
+  __shared__ int32_t s_pre[kPoolThreads + 1];
+  __shared__ int32_t s_slot[kPoolThreads];
   __shared__ int64_t s_pos;
   __shared__ int32_t s_end;
+  __shared__ int32_t s_bad;
   const int32_t t = threadIdx.x;
   Cursor c{v.meta[0], v.meta[1], v.meta[2]};
   int32_t err = 0;
@@ -198,54 +244,111 @@ __global__ __launch_bounds__(kPoolThreads) void pool_apply_kernel(
   while (i < num_ops) {
     const int4 op = ops[i];
     if (op.x == NKV_POOL_OP_APPEND) {
-      // A run of consecutive appends [i, j): one parallel pop.
-      if (t == 0) s_end = 0x7fffffff;
+      // A run of appends to distinct slots: one parallel pop for its valid
+      // prefix; the first invalid op (or the first that finds no free
+      // block) stops the log, as it would one op at a time.
+      int4 mine;
+      const int32_t run = run_length(
+          v, ops, i, num_ops, [](const int4& o) { return o.x == NKV_POOL_OP_APPEND; }, &s_end,
+          &mine);
+      if (t == 0) s_bad = run;
       __syncthreads();
-      int64_t j = i;
-      for (int64_t base = i; base < num_ops; base += kPoolThreads) {
-        const int64_t k = base + t;
-        if (k < num_ops && ops[k].x != NKV_POOL_OP_APPEND) {
-          atomicMin(&s_end, static_cast<int32_t>(k - i));
+      int32_t code = 0;
+      if (t < run) {
+        if (mine.y < 0 || mine.y >= v.max_seqs) {
+          code = kErrBadSlot;
+        } else if (v.nblk[mine.y] >= v.width) {
+          code = kErrTableFull;
         }
-        __syncthreads();
-        const int32_t end = s_end;
-        __syncthreads();
-        if (end != 0x7fffffff) {
-          j = i + end;
-          break;
-        }
-        j = min(base + kPoolThreads, num_ops);
+        if (code != 0) atomicMin(&s_bad, t);
       }
-      const int64_t m = j - i;
-      int32_t bad_slot = 0, full = 0;
-      for (int64_t base = 0; base < m; base += kPoolThreads) {
-        int32_t my_bad = 0, my_full = 0;
-        if (base + t < m) {
-          const int32_t slot = ops[i + base + t].y;
-          if (slot < 0 || slot >= v.max_seqs) {
-            my_bad = 1;
-          } else if (v.nblk[slot] >= v.width) {
-            my_full = 1;
-          }
-        }
-        bad_slot += block_count(my_bad, s_tmp);
-        full += block_count(my_full, s_tmp);
-      }
-      if (bad_slot != 0 || full != 0 || m > c.live) {
-        err = bad_slot != 0 ? kErrBadSlot : full != 0 ? kErrTableFull : kErrNoFreeBlocks;
-        err_op = i;
-        break;
-      }
-      pop_front(v, c, static_cast<int32_t>(m), s_tmp, &s_pos, [&](int32_t k, int32_t b) {
-        const int32_t slot = ops[i + k].y;
+      __syncthreads();
+      const int32_t first_bad = s_bad;
+      if (t == first_bad && first_bad < run) s_bad = code;  // broadcast its code
+      __syncthreads();
+      const int32_t bad_code = first_bad < run ? s_bad : 0;
+      const int32_t ok = static_cast<int32_t>(min<int64_t>(first_bad, c.live));
+      if (t < ok) s_slot[t] = mine.y;
+      __syncthreads();
+      pop_front(v, c, ok, s_tmp, &s_pos, [&](int32_t k, int32_t b) {
+        const int32_t slot = s_slot[k];
         const int32_t pos = v.nblk[slot];
         v.tables[static_cast<int64_t>(slot) * v.width + pos] = b;
         v.nblk[slot] = pos + 1;
         v.ref[b] = 1;
       });
       __syncthreads();
-      i = j;
+      if (ok < run) {
+        err = ok == first_bad ? bad_code : kErrNoFreeBlocks;
+        err_op = i + ok;
+        break;
+      }
+      i += run;
       continue;
+    }
+
+    if (op.x == NKV_POOL_OP_ALLOCATE) {
+      // A run of allocations without cached-prefix ids, to distinct slots:
+      // the run's fresh blocks are one parallel pop in op order.
+      int4 mine;
+      const int32_t run = run_length(
+          v, ops, i, num_ops,
+          [&](const int4& o) {
+            return o.x == NKV_POOL_OP_ALLOCATE && o.w >= 0 && o.w < num_args && args[o.w] == 0;
+          },
+          &s_end, &mine);
+      if (run > 0) {
+        if (t == 0) s_bad = run;
+        __syncthreads();
+        int32_t code = 0;
+        if (t < run) {
+          if (mine.y < 0 || mine.y >= v.max_seqs) {
+            code = kErrBadSlot;
+          } else if (v.nblk[mine.y] != 0) {
+            code = kErrTableBusy;
+          } else if (mine.z < 0 || mine.z > v.width) {
+            code = kErrBadArgs;
+          }
+          if (code != 0) atomicMin(&s_bad, t);
+        }
+        __syncthreads();
+        const int32_t first_bad = s_bad;
+        if (t == first_bad && first_bad < run) s_bad = code;
+        __syncthreads();
+        const int32_t bad_code = first_bad < run ? s_bad : 0;
+        // Fresh blocks needed up to each op, over the valid prefix.
+        int32_t total = 0;
+        const int32_t need = t < first_bad ? mine.z : 0;
+        const int32_t before = block_exclusive_scan<kPoolThreads>(need, s_tmp, &total);
+        if (t < run) {
+          s_pre[t] = before;
+          s_slot[t] = mine.y;
+        }
+        if (t == 0) s_end = first_bad;
+        __syncthreads();
+        // The first op whose blocks would not all be free.
+        if (t < first_bad && before + need > c.live) atomicMin(&s_end, t);
+        __syncthreads();
+        const int32_t fits = s_end;
+        const int32_t ok = min(first_bad, fits);
+        if (t == 0) s_pre[ok] = ok < run ? s_pre[ok] : total;
+        __syncthreads();
+        const int32_t pops = s_pre[ok];
+        pop_front(v, c, pops, s_tmp, &s_pos, [&](int32_t x, int32_t b) {
+          const int32_t k = owner_of(s_pre, ok, x);
+          v.tables[static_cast<int64_t>(s_slot[k]) * v.width + (x - s_pre[k])] = b;
+          v.ref[b] = 1;
+        });
+        if (t < ok) v.nblk[s_slot[t]] = s_pre[t + 1] - s_pre[t];
+        __syncthreads();
+        if (ok < run) {
+          err = ok == first_bad ? bad_code : kErrNoFreeBlocks;
+          err_op = i + ok;
+          break;
+        }
+        i += run;
+        continue;
+      }
     }
 
     const int32_t slot = op.y;
@@ -404,9 +507,9 @@ int check_desc(const nkv_pool_desc* d, const char* what) {
 extern "C" int64_t nkv_pool_bytes(int64_t num_blocks, int64_t max_seqs,
                                   int64_t max_blocks_per_seq) {
   if (!nkv::geometry_ok(num_blocks, max_seqs, max_blocks_per_seq)) return 0;
-  int64_t off[7];
+  int64_t off[8];
   nkv::pool_layout(num_blocks, max_seqs, max_blocks_per_seq, off);
-  return off[6];
+  return off[7];
 }
 
 extern "C" int nkv_pool_offsets(int64_t num_blocks, int64_t max_seqs,
@@ -415,7 +518,7 @@ extern "C" int nkv_pool_offsets(int64_t num_blocks, int64_t max_seqs,
   if (!nkv::geometry_ok(num_blocks, max_seqs, max_blocks_per_seq)) {
     return nkv_fail(NKV_E_INVALID, "nkv_pool_offsets: bad geometry");
   }
-  int64_t off[7];
+  int64_t off[8];
   nkv::pool_layout(num_blocks, max_seqs, max_blocks_per_seq, off);
   for (int k = 0; k < 6; ++k) offsets[k] = off[k];
   return NKV_OK;

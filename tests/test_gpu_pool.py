@@ -240,6 +240,89 @@ def test_invalid_ops_stop_the_log_and_keep_the_state(gpu_device):
     assert pool.error() is None
 
 
+def sequential(oracle, ops, width, max_seqs):
+    """The op log one op at a time on the oracle, stopping at the first
+    invalid op: returns (index, code) of that op, or None."""
+    for idx, op in enumerate(ops):
+        kind, slot = op[0], op[1]
+        if kind == "fence":
+            continue
+        if not 0 <= slot < max_seqs:
+            return idx, 2
+        if kind == "allocate":
+            n, cached = op[2], op[3]
+            if oracle.table(slot):
+                return idx, 3
+            if not 0 <= n <= width or len(cached) > n:
+                return idx, 7
+            hits_free = sum(1 for b in cached if oracle.ref[b] == 0)
+            if oracle.num_free() - hits_free < n - len(cached):
+                return idx, 5
+            oracle.allocate(slot, n, cached)
+        elif kind == "append":
+            if len(oracle.table(slot)) >= width:
+                return idx, 4
+            if oracle.num_free() < 1:
+                return idx, 5
+            oracle.append(slot)
+        else:
+            oracle.deallocate(slot)
+    return None
+
+
+def raw_log(pool, ops):
+    """Writes ops straight into the pool's log (no recorder checks, no
+    fences), as a C caller could."""
+    from nanokv import _lib
+
+    codes = {"allocate": _lib.NKV_POOL_OP_ALLOCATE, "deallocate": _lib.NKV_POOL_OP_DEALLOCATE,
+             "append": _lib.NKV_POOL_OP_APPEND, "fence": _lib.NKV_POOL_OP_FENCE}
+    for op in ops:
+        if op[0] == "allocate":
+            pool._ops.append((codes["allocate"], op[1], op[2], len(pool._args)))
+            pool._args.extend([len(op[3]), *op[3]])
+        else:
+            pool._ops.append((codes[op[0]], op[1], 0, 0))
+
+
+@pytest.mark.parametrize("case", [
+    # appends repeating a slot inside one run
+    [("append", 0), ("append", 1), ("append", 0), ("append", 2), ("append", 0), ("append", 1)],
+    # allocations without cached ids repeating a slot (the repeat is busy)
+    [("allocate", 4, 2, []), ("allocate", 5, 1, []), ("allocate", 4, 1, []), ("allocate", 6, 1, [])],
+    # a bad slot in the middle of an append run
+    [("append", 0), ("append", 1), ("append", 11), ("append", 2)],
+    # an append past the table width in the middle of a run
+    [("append", 3), ("append", 3), ("append", 3), ("append", 3), ("append", 3), ("append", 1)],
+    # more appends than free blocks
+    [("append", s % 4) for s in range(40)],
+    # allocations whose running total passes the free count
+    [("allocate", 4, 3, []), ("allocate", 5, 4, []), ("allocate", 6, 4, []), ("allocate", 7, 1, [])],
+    # bad sizes inside an allocation run
+    [("allocate", 4, 2, []), ("allocate", 5, 9, []), ("allocate", 6, 1, [])],
+    # runs split by other ops
+    [("allocate", 4, 1, []), ("append", 4), ("deallocate", 0), ("allocate", 0, 2, []),
+     ("append", 0), ("fence", 0), ("append", 0), ("allocate", 5, 1, [4])],
+])
+def test_runs_match_one_op_at_a_time(gpu_device, case):
+    width, max_seqs, nb = 5, 8, 14
+    pool = make_pool(gpu_device, nb, max_seqs=max_seqs, width=width)
+    oracle = BlockPoolOracle(nb, width)
+    for s in range(4):  # slots 0..3 hold one block each; 10 free
+        pool.allocate(s, 1)
+        oracle.allocate(s, 1)
+    pool.flush()
+    assert_same(pool, oracle, "setup")
+    expected_err = sequential(oracle, case, width, max_seqs)
+    raw_log(pool, case)
+    pool.flush()
+    snap = pool.snapshot()
+    assert snap["error"] == expected_err
+    assert snap["queue"] == oracle.queue()
+    assert snap["ref"] == oracle.ref
+    assert snap["tables"] == {s: t for s, t in oracle.tables.items() if t}
+
+
 def test_host_side_checks(gpu_device):
     pool = make_pool(gpu_device, 8, max_seqs=4, width=4)
     with pytest.raises(ValueError):
