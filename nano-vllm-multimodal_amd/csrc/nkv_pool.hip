@@ -351,6 +351,65 @@ __global__ __launch_bounds__(kPoolThreads) void pool_apply_kernel(
       }
     }
 
+    if (op.x == NKV_POOL_OP_DEALLOCATE) {
+      // A run of deallocations to distinct slots whose blocks are all held
+      // once (no shared prefix): every block is freed, in op order and
+      // reversed table order, so one pass places them all.  Anything else
+      // (a shared or invalid block, a bad slot) takes the one-op path.
+      int4 mine;
+      const int32_t run = run_length(
+          v, ops, i, num_ops, [](const int4& o) { return o.x == NKV_POOL_OP_DEALLOCATE; },
+          &s_end, &mine);
+      const bool slot_ok = t < run && mine.y >= 0 && mine.y < v.max_seqs;
+      const int32_t n = slot_ok ? min(max(v.nblk[mine.y], 0), v.width) : 0;
+      int32_t total = 0;
+      const int32_t before = block_exclusive_scan<kPoolThreads>(n, s_tmp, &total);
+      const int32_t bad_slots = block_count(t < run && !slot_ok ? 1 : 0, s_tmp);
+      if (t < run) {
+        s_pre[t] = before;
+        s_slot[t] = mine.y;
+      }
+      if (t == 0) s_pre[run] = total;
+      __syncthreads();
+      int32_t unshared = 0;
+      for (int32_t base = 0; base < total; base += kPoolThreads) {
+        int32_t ok = 1;
+        const int32_t x = base + t;
+        if (x < total) {
+          const int32_t k = owner_of(s_pre, run, x);
+          const int32_t nk = s_pre[k + 1] - s_pre[k];
+          const int32_t b =
+              v.tables[static_cast<int64_t>(s_slot[k]) * v.width + (nk - 1 - (x - s_pre[k]))];
+          ok = (b >= 0 && b < v.num_blocks && v.ref[b] == 1) ? 1 : 0;
+        }
+        unshared += block_count(ok, s_tmp);
+      }
+      if (bad_slots == 0 && unshared == (total + kPoolThreads - 1) / kPoolThreads * kPoolThreads) {
+        if (c.tail - c.head + total > v.cap) compact(v, c, s_tmp);
+        for (int32_t base = 0; base < total; base += kPoolThreads) {
+          const int32_t x = base + t;
+          if (x < total) {
+            const int32_t k = owner_of(s_pre, run, x);
+            const int32_t nk = s_pre[k + 1] - s_pre[k];
+            int32_t* cell =
+                v.tables + static_cast<int64_t>(s_slot[k]) * v.width + (nk - 1 - (x - s_pre[k]));
+            const int32_t b = *cell;
+            const int64_t pos = c.tail + x;
+            v.ring[pos % v.cap] = b;
+            v.qpos[b] = pos;
+            v.ref[b] = 0;
+            *cell = -1;
+          }
+        }
+        if (t < run) v.nblk[mine.y] = 0;
+        c.tail += total;
+        c.live += total;
+        __syncthreads();
+        i += run;
+        continue;
+      }
+    }
+
     const int32_t slot = op.y;
     if (slot < 0 || slot >= v.max_seqs) {
       err = kErrBadSlot;

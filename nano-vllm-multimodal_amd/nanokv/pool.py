@@ -134,10 +134,11 @@ class DeviceBlockPool:
     def pending_ops(self) -> int:
         return len(self._ops)
 
-    def flush(self) -> None:
+    def flush(self, timer=None) -> None:
         """Replay the recorded calls on the device (current stream), in
         order, and start a new log.  The pinned staging buffer is reused once
-        the previous upload has completed."""
+        the previous upload has completed.  `timer` (a
+        nanokv.benchmark.LaunchTimer) brackets the apply kernel alone."""
         if not self._ops:
             return
         ops = np.asarray(self._ops, dtype=np.int32).reshape(-1)
@@ -155,10 +156,13 @@ class DeviceBlockPool:
         if self._uploaded is None:
             self._uploaded = torch.cuda.Event()
         self._uploaded.record(torch.cuda.current_stream(self.device))
+        started = timer.start() if timer is not None else None
         status = _lib.load_library().nkv_pool_apply(
             ctypes.byref(self._desc), device_log.data_ptr(), len(self._ops),
             device_log[ops.size:].data_ptr(), args.size, self._stream(),
         )
+        if timer is not None:
+            timer.stop(started)
         _lib.check(status, "nkv_pool_apply")
         self._ops.clear()
         self._args.clear()

@@ -303,6 +303,12 @@ def raw_log(pool, ops):
     # runs split by other ops
     [("allocate", 4, 1, []), ("append", 4), ("deallocate", 0), ("allocate", 0, 2, []),
      ("append", 0), ("fence", 0), ("append", 0), ("allocate", 5, 1, [4])],
+    # a deallocation run (no sharing), with a repeat and an empty slot
+    [("append", 1), ("deallocate", 0), ("deallocate", 1), ("deallocate", 0), ("deallocate", 6),
+     ("deallocate", 2)],
+    # a deallocation run over a shared block (one-op path), then a bad slot
+    [("allocate", 4, 2, [1]), ("allocate", 5, 3, [1, 0]), ("deallocate", 1), ("deallocate", 4),
+     ("deallocate", 0), ("deallocate", 5), ("deallocate", 9)],
 ])
 def test_runs_match_one_op_at_a_time(gpu_device, case):
     width, max_seqs, nb = 5, 8, 14
