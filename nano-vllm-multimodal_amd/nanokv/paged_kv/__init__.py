@@ -36,6 +36,21 @@ def create_paged_kv_backend(name: str) -> PagedKVBackend:
     raise ValueError(f"unknown paged KV backend: {name}")
 
 
+_DEFAULT_BACKEND = None
+
+
+def store_kvcache(key, value, k_cache, v_cache, slot_mapping) -> None:
+    """The legacy store entry point of the attention layer
+    (nanovllm/layers/attention.py:10-33, hard-wired to the Triton backend
+    there), on the ``hip`` backend: write this step's K/V rows [N, H, D]
+    into the paged caches at slot_mapping, skipping -1.  Attention.forward
+    calls it when no backend is bound and the caches are (:86-93)."""
+    global _DEFAULT_BACKEND
+    if _DEFAULT_BACKEND is None:
+        _DEFAULT_BACKEND = create_paged_kv_backend("hip")
+    _DEFAULT_BACKEND.store(key, value, k_cache, v_cache, slot_mapping)
+
+
 __all__ = [
     "BACKEND_NAMES",
     "GatherDimensions",
@@ -45,6 +60,7 @@ __all__ = [
     "create_paged_kv_backend",
     "index_value_validation_enabled",
     "resolve_paged_kv_backend_name",
+    "store_kvcache",
     "validate_gather_inputs",
     "validate_store_inputs",
 ]

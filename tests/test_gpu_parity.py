@@ -80,6 +80,27 @@ def test_fused_qkv_strided_key_seed29(backend, gpu_device):
     np.testing.assert_array_equal(words(vc), hv)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_legacy_store_kvcache_on_fused_qkv(gpu_device, dtype):
+    """attention.py:10-33 / :86-93: the layer's fallback store when no
+    backend is bound, called with the K/V views of the fused QKV output."""
+    from nanokv.paged_kv import store_kvcache
+
+    torch.manual_seed(31)
+    heads_q, heads_kv, dim = 8, 2, 128
+    qkv = torch.randn(13, (heads_q + 2 * heads_kv) * dim, device=gpu_device, dtype=dtype)
+    _, k, v = qkv.split([heads_q * dim, heads_kv * dim, heads_kv * dim], dim=-1)
+    k, v = k.view(-1, heads_kv, dim), v.view(-1, heads_kv, dim)
+    slots = torch.tensor([5, -1, 0, 63, 17, -1, 40, 2, 33, 48, 9, 61, 26], dtype=torch.int32, device=gpu_device)
+    kc = torch.full((4, 16, heads_kv, dim), -3, device=gpu_device, dtype=dtype)
+    vc = torch.full_like(kc, -3)
+    hk, hv = oracle_store(k, v, kc, vc, slots)
+    store_kvcache(k, v, kc, vc, slots)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(words(kc), hk)
+    np.testing.assert_array_equal(words(vc), hv)
+
+
 def test_full_parity_matrix_seed23(backend, gpu_device):
     torch.manual_seed(23)
     num_blocks, block_size = 41, 16

@@ -154,6 +154,19 @@ class BackendResolutionTests(unittest.TestCase):
         with self.assertRaisesRegex(ValueError, "dtype"):
             backend.allocate((2, 1, 4, 2, 4), dtype=torch.int8, device="cuda")
 
+    def test_legacy_store_kvcache_keeps_signature_and_contract(self):
+        import inspect
+
+        from nanokv.paged_kv import store_kvcache
+
+        # attention.py:10-16: store_kvcache(key, value, k_cache, v_cache, slot_mapping)
+        self.assertEqual(len(inspect.signature(store_kvcache).parameters), 5)
+        key, value, key_cache, value_cache, slots = store_inputs()
+        with self.assertRaisesRegex(ValueError, "matching shape"):
+            store_kvcache(key[:2], value, key_cache, value_cache, slots)
+        with self.assertRaisesRegex(ValueError, "ROCm"):
+            store_kvcache(key, value, key_cache, value_cache, slots)
+
 
 if __name__ == "__main__":
     unittest.main()
