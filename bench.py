@@ -20,6 +20,10 @@ timed step replaces the gather by its consumer, paged-attention decode read
 straight from the cache (16 query heads), reported under "attention", and
 "block_pool" times the same steps' block bookkeeping replayed on the device
 block pool (with the host restatement's time in the CPU leg).
+"copy_reference" times a plain device copy of the gather's payload and the
+gather over contiguous block tables; "other_workloads" times the
+single-layer store / gather configurations (decode store, chunked-prefill
+store, prefix-cache gather, narrow rows) kernel by kernel.
 """
 from __future__ import annotations
 
@@ -67,6 +71,8 @@ def parse_args(argv=None):
     p.add_argument("--cpu-baseline-layers", type=int, default=28,
                    help="layers in the CPU baseline sample (0 disables it)")
     p.add_argument("--cpu-baseline-repeats", type=int, default=9)
+    p.add_argument("--workload-iterations", type=int, default=30,
+                   help="timed launches per operation of the single-layer configurations; 0 = skip")
     p.add_argument("--profile", action="store_true",
                    help="run warmup + timed steps only (no check, no CPU baseline), for rocprofv3")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -213,9 +219,22 @@ def main(argv=None) -> int:
     gather_mean = sum(gather_us) / len(gather_us)
     achieved = gather_launch_bytes / (gather_mean * 1e-6) / 1e9
 
+    copy_reference = measure_copy_reference(wl, device, backend, packer, cache, total, k_out, v_out,
+                                            args.steps)
+    log(f"[bench] copy reference: torch copy_ {copy_reference['torch_copy_gbps']:.0f} GB/s, "
+        f"gather over contiguous tables {copy_reference['gather_contiguous_tables_gbps']:.0f} GB/s")
+
     block_pool = measure_block_pool(wl, device, packer, batch, args.steps, args.warmup)
     log(f"[bench] block pool: apply {block_pool['apply_kernel_us']:.1f} us, step "
         f"{block_pool['stream_us_per_step']:.1f} us stream / {block_pool['host_us_per_step']:.1f} us host")
+
+    other_workloads = None
+    if args.workload_iterations > 0 and not args.profile:
+        other_workloads = measure_other_workloads(device, args.workload_iterations)
+        for r in other_workloads:
+            if r["gbps_at_p50"] is not None:
+                log(f"[bench] {r['workload']} {r['operation']}: p50 {r['p50_us']:.2f} us, "
+                    f"{r['gbps_at_p50']:.0f} GB/s")
 
     traffic = measured_traffic(TRAFFIC_FILE, wl.gather_bytes(layers=1))
     attn_traffic = measured_traffic(ATTENTION_TRAFFIC_FILE, attn_bytes)
@@ -313,6 +332,8 @@ def main(argv=None) -> int:
             "step_ms_store_attention": round(attn_step_ms, 4),
             "decode_tokens_per_s_store_attention": round(B / (attn_step_ms * 1e-3), 2),
         },
+        "copy_reference": copy_reference,
+        "other_workloads": other_workloads,
         "block_pool": block_pool,
         "cpu_baseline": cpu_baseline,
         "host": {"platform": platform.platform(), "torch": torch.__version__, "hip": torch.version.hip,
@@ -320,6 +341,91 @@ def main(argv=None) -> int:
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+OTHER_WORKLOADS = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows")
+
+
+def measure_other_workloads(device, iterations: int) -> list[dict]:
+    """The single-layer store / gather configurations of the paged-KV
+    micro-benchmark (decode store, chunked-prefill store, prefix-cache
+    gather, narrow rows), each on its own cache, with the MALL evicted by a
+    512 MiB read before every timed launch.  One compact record per
+    operation that moves bytes."""
+    import torch
+
+    from nanokv.benchmark import run_workload
+
+    records = []
+    for name in OTHER_WORKLOADS:
+        for r in run_workload(name, iterations=iterations, warmup=5, device=device):
+            if r["algorithmic_bytes"] == 0:
+                continue
+            records.append({
+                "workload": name, "operation": r["operation"],
+                "algorithmic_bytes": r["algorithmic_bytes"],
+                "p50_us": round(r["latency"]["p50_us"], 2),
+                "gbps_at_p50": r["gbps_at_p50"], "hbm_fraction": r["hbm_fraction"],
+            })
+        torch.cuda.empty_cache()
+    return records
+
+
+def measure_copy_reference(wl, device, backend, packer, cache, total, k_out, v_out, reps: int) -> dict:
+    """Context for the gather's roofline fraction, on the same payload (one
+    layer's K and V contexts, read once and written once):
+    - the runtime's plain device-to-device copy (torch ``copy_``) of a
+      contiguous buffer of that size;
+    - the gather itself over block tables that place every sequence's blocks
+      back to back in the cache, so only the block-table indirection differs
+      from the copy of contiguous memory."""
+    import numpy as np
+    import torch
+
+    from nanokv.benchmark import LaunchTimer
+    from nanokv.packing import SequenceBatch
+
+    stream = torch.cuda.current_stream(device)
+    payload = 2 * k_out.numel() * k_out.element_size()
+    src = torch.ones(payload // 2, dtype=torch.int16, device=device)
+    dst = torch.empty_like(src)
+    copy_timer = LaunchTimer(stream)
+    for i in range(reps + 2):
+        t0 = copy_timer.start() if i >= 2 else None
+        dst.copy_(src)
+        if t0 is not None:
+            copy_timer.stop(t0)
+    copy_us = copy_timer.durations_us()
+    del src, dst
+
+    counts = -(-wl.num_tokens.astype(np.int64) // wl.block_size)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    if offsets[-1] > wl.num_blocks:
+        raise RuntimeError("the contiguous layout needs more blocks than the cache holds")
+    batch = SequenceBatch(wl.num_tokens, offsets, np.arange(offsets[-1]))
+    ctx = packer.pack_decode(batch)
+    kc, vc = cache[0, 0], cache[1, 0]
+    plan = backend.build_gather_plan(kc, ctx.block_tables, ctx.cu_seqlens_k, total)
+    gather_timer = LaunchTimer(stream)
+    for i in range(reps + 2):
+        t0 = gather_timer.start() if i >= 2 else None
+        backend.gather_varlen(kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
+                              plan=plan, out=(k_out, v_out))
+        if t0 is not None:
+            gather_timer.stop(t0)
+    gather_us = gather_timer.durations_us()
+    torch.cuda.synchronize()
+    copy_mean = float(np.mean(copy_us))
+    gather_mean = float(np.mean(gather_us))
+    return {
+        "payload_bytes": payload,
+        "torch_copy_us": round(copy_mean, 2),
+        "torch_copy_gbps": round(2 * payload / (copy_mean * 1e-6) / 1e9, 2),
+        "gather_contiguous_tables_us": round(gather_mean, 2),
+        "gather_contiguous_tables_gbps": round(wl.gather_bytes(layers=1) / (gather_mean * 1e-6) / 1e9, 2),
+        "note": "bytes counted as read + write of the payload; the gather's figure uses its "
+                "algorithmic bytes (payload read + written, plus block ids)",
+    }
 
 
 def block_pool_steps(wl, seed: int = 11):

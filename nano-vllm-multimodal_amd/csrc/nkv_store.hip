@@ -27,6 +27,15 @@ namespace {
 
 constexpr int kStoreThreads = NKV_STORE_THREADS;
 
+// Words per lane issued together: one workgroup's NKV_STORE_WG_BYTES in one
+// batch, so a lane waits for memory twice per batch (its rows' slots, then
+// its words) instead of twice per word.
+template <int W>
+constexpr int store_batch() {
+  return NKV_STORE_WG_BYTES / (W * kStoreThreads) > 0
+             ? NKV_STORE_WG_BYTES / (W * kStoreThreads) : 1;
+}
+
 template <int W>
 __global__ __launch_bounds__(kStoreThreads) void store_rows_kernel(
     const uint8_t* __restrict__ key, const uint8_t* __restrict__ value,
@@ -35,19 +44,36 @@ __global__ __launch_bounds__(kStoreThreads) void store_rows_kernel(
     int64_t key_stride, int64_t value_stride, int64_t row_bytes,
     int32_t row_words, int32_t rows_per_wg, int64_t num_slots) {
   using T = typename Word<W>::type;
+  constexpr int U = store_batch<W>();
   const bool second = blockIdx.y != 0;
   const uint8_t* src = second ? value : key;
   const int64_t stride = second ? value_stride : key_stride;
   uint8_t* dst = second ? value_cache : key_cache;
   const int32_t t0 = blockIdx.x * rows_per_wg;  // < num_tokens by the grid
   const int32_t nwords = min(rows_per_wg, num_tokens - t0) * row_words;
-  for (int32_t w = threadIdx.x; w < nwords; w += kStoreThreads) {
-    const int32_t r = w / row_words;
-    const int32_t c = w - r * row_words;
-    const int32_t slot = slot_mapping[t0 + r];
-    if (slot < 0 || slot >= num_slots) continue;  // -1 padding (and garbage)
-    const T v = load_stream(reinterpret_cast<const T*>(src + (t0 + r) * stride) + c);
-    store_stream(reinterpret_cast<T*>(dst + slot * row_bytes) + c, v);
+  for (int32_t base = 0; base < nwords; base += U * kStoreThreads) {
+    int32_t row[U], col[U], slot[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int32_t w = base + u * kStoreThreads + static_cast<int32_t>(threadIdx.x);
+      row[u] = w / row_words;
+      col[u] = w - row[u] * row_words;
+      slot[u] = w < nwords ? slot_mapping[t0 + row[u]] : -1;
+    }
+    T v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // -1 padding (and any slot outside the cache) moves nothing
+      if (slot[u] >= 0 && slot[u] < num_slots) {
+        v[u] = load_stream(reinterpret_cast<const T*>(src + (t0 + row[u]) * stride) + col[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (slot[u] >= 0 && slot[u] < num_slots) {
+        store_stream(reinterpret_cast<T*>(dst + slot[u] * row_bytes) + col[u], v[u]);
+      }
+    }
   }
 }
 

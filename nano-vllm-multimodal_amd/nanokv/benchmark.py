@@ -86,15 +86,18 @@ FLUSH_BYTES = 512 << 20  # > the 256 MB MALL
 
 def _time_with_flush(fn, flush: torch.Tensor, iterations: int, warmup: int) -> list[float]:
     """Per-iteration event timing of ``fn``; before each timed call a
-    512 MiB fill evicts the MALL / L2, so re-reads cannot be served from
-    on-die caches.  The fill is outside the bracketed region."""
+    512 MiB read (a sum over the flush buffer) evicts the MALL / L2, so
+    re-reads cannot be served from on-die caches.  The eviction reads rather
+    than writes, so the timed call does not pay for writing back dirty lines
+    it did not make.  The read is outside the bracketed region."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
+    words = flush.view(torch.int64)
     pairs = []
-    for i in range(iterations):
-        flush.fill_(i & 0x7F)
+    for _ in range(iterations):
+        words.sum()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record(stream)
@@ -121,7 +124,7 @@ def run_workload(name: str, *, iterations: int = 50, warmup: int = 5, device=Non
     shape = (wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim)
     kc = torch.empty(shape, dtype=wl.dtype, device=device).normal_()
     vc = torch.empty_like(kc).normal_()
-    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=device)
+    flush = torch.zeros(FLUSH_BYTES, dtype=torch.uint8, device=device)
     element = torch.empty((), dtype=wl.dtype).element_size()
     records = []
 
