@@ -111,6 +111,7 @@ def test_long_contexts_over_small_blocks(backend, gpu_device, hkv, g, bs):
         own = entries[entries[:, 2] == i]
         assert own[:, 0].tolist() == list(range(0, n, rows))
         assert int(own[:, 1].sum()) == n
+    assert not plan.cpu().numpy()[sum(expect_entries):, 1].any()  # entries past the total are empty
     out = backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev["tables"], dev["cu"],
                                          total, 1 / math.sqrt(128), plan=(plan, first))
     ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], host["tables"],
