@@ -23,7 +23,9 @@ block pool (with the host restatement's time in the CPU leg).
 "copy_reference" times a plain device copy of the gather's payload and the
 gather over contiguous block tables; "other_workloads" times the
 single-layer store / gather configurations (decode store, chunked-prefill
-store, prefix-cache gather, narrow rows) kernel by kernel.
+store, prefix-cache gather, narrow rows) kernel by kernel; "gpu_reference"
+runs the reference pytorch backend's torch ops on the same GPU, on the
+decode step and on the reference's own store/gather microbenchmark matrix.
 """
 from __future__ import annotations
 
@@ -73,6 +75,8 @@ def parse_args(argv=None):
     p.add_argument("--cpu-baseline-repeats", type=int, default=9)
     p.add_argument("--workload-iterations", type=int, default=30,
                    help="timed launches per operation of the single-layer configurations; 0 = skip")
+    p.add_argument("--no-gpu-reference", dest="gpu_reference", action="store_false",
+                   help="skip the torch restatement of the reference pytorch backend on the GPU")
     p.add_argument("--profile", action="store_true",
                    help="run warmup + timed steps only (no check, no CPU baseline), for rocprofv3")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -228,6 +232,20 @@ def main(argv=None) -> int:
     log(f"[bench] block pool: apply {block_pool['apply_kernel_us']:.1f} us, step "
         f"{block_pool['stream_us_per_step']:.1f} us stream / {block_pool['host_us_per_step']:.1f} us host")
 
+    gpu_reference = None
+    if args.gpu_reference and not args.profile:
+        gpu_reference = {
+            "what": "the reference pytorch backend's store/gather restated with its torch ops "
+                    "(index_copy_ / index_select), driven as the reference's SDPA decode drives it, "
+                    "on the same GPU",
+            "decode_step": measure_torch_reference_step(wl, device, cache, new_k, new_v, batch,
+                                                        packer, step_ms),
+            "microbenchmark": measure_reference_matrix(device, backend),
+        }
+        log(f"[bench] torch reference decode step: "
+            f"{gpu_reference['decode_step']['ms_per_step']:.1f} ms/step "
+            f"({gpu_reference['decode_step']['speedup_of_hip']:.1f}x slower than hip)")
+
     other_workloads = None
     if args.workload_iterations > 0 and not args.profile:
         other_workloads = measure_other_workloads(device, args.workload_iterations)
@@ -334,6 +352,7 @@ def main(argv=None) -> int:
         },
         "copy_reference": copy_reference,
         "other_workloads": other_workloads,
+        "gpu_reference": gpu_reference,
         "block_pool": block_pool,
         "cpu_baseline": cpu_baseline,
         "host": {"platform": platform.platform(), "torch": torch.__version__, "hip": torch.version.hip,
@@ -538,6 +557,163 @@ def measure_block_pool(wl, device, packer, batch, steps: int, warmup: int) -> di
         "note": "stream_us brackets the whole step with events, so it includes the host's "
                 "launch gaps; apply_kernel_us brackets the apply kernel alone",
     }
+
+
+def torch_reference_backend():
+    """The reference's ``pytorch`` paged-KV backend
+    (nanovllm/layers/paged_kv/pytorch_backend.py:26-50) restated with the
+    same validators and the same torch ops, for timing on the GPU beside the
+    hip backend: the store masks out -1 slots (a device-to-host sync) and
+    scatters with ``index_copy_``; the gather copies whole blocks with
+    ``index_select`` and slices them to the length."""
+    import torch
+
+    from nanokv.paged_kv import validate_gather_inputs, validate_store_inputs
+
+    class TorchReferenceBackend:
+        name = "torch-reference"
+
+        def store(self, key, value, key_cache, value_cache, slot_mapping):
+            validate_store_inputs(key, value, key_cache, value_cache, slot_mapping)
+            keep = slot_mapping >= 0
+            rows = slot_mapping[keep].to(dtype=torch.long)
+            key_cache.flatten(0, 1).index_copy_(0, rows, key[keep])
+            value_cache.flatten(0, 1).index_copy_(0, rows, value[keep])
+
+        def gather(self, cache, block_table, sequence_length):
+            dims = validate_gather_inputs(cache, block_table, sequence_length)
+            if dims.required_blocks == 0:
+                return cache.new_empty((0, dims.num_kv_heads, dims.head_dim))
+            ids = block_table[: dims.required_blocks].to(dtype=torch.long)
+            return cache.index_select(0, ids).flatten(0, 1)[:sequence_length]
+
+    return TorchReferenceBackend()
+
+
+def measure_torch_reference_step(wl, device, cache, new_k, new_v, batch, packer,
+                                 hip_step_ms: float, steps: int = 2) -> dict:
+    """The decode step's data path as the reference's SDPA decode drives its
+    backend (nanovllm/layers/attention.py:75-93, 284-300): per layer one
+    store, then per sequence a host read of its context length and one
+    gather each of K and V.  The packed metadata is the same as the hip
+    step's (packed once, outside the timed region; the reference packs on
+    the host).  The outputs are dropped where SDPA would consume them."""
+    import torch
+
+    ref = torch_reference_backend()
+    ctx = packer.pack_decode(batch)
+    torch.cuda.synchronize()
+
+    def step():
+        for layer in range(wl.num_layers):
+            kc, vc = cache[0, layer], cache[1, layer]
+            ref.store(new_k[layer], new_v[layer], kc, vc, ctx.slot_mapping)
+            for i in range(wl.num_seqs):
+                n = int(ctx.context_lens[i])
+                ref.gather(kc, ctx.block_tables[i], n)
+                ref.gather(vc, ctx.block_tables[i], n)
+
+    step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {
+        "ms_per_step": round(ms, 2),
+        "decode_tokens_per_s": round(wl.num_seqs / (ms * 1e-3), 2),
+        "store_gather_gbps": round((wl.store_bytes() + wl.gather_bytes()) / (ms * 1e-3) / 1e9, 2),
+        "speedup_of_hip": round(ms / hip_step_ms, 2),
+        "steps": steps,
+        "timing": "host wall clock over whole steps (the per-sequence length reads synchronize)",
+    }
+
+
+REFERENCE_MATRIX = {  # bench_paged_kv.py's defaults in the reference
+    "operations": ("store", "gather"), "dtypes": ("float16", "bfloat16"), "tokens": (1, 8, 257),
+    "kv_shapes": ((1, 64), (2, 128), (8, 128)), "num_blocks": 64, "block_size": 16,
+    "mapping": "random_with_skips", "seed": 17, "warmup": 100, "iterations": 1000,
+}
+
+
+def measure_reference_matrix(device, backend, iterations: int | None = None) -> dict:
+    """The reference's store/gather microbenchmark matrix
+    (nanovllm/benchmark/paged_kv.py:163-197, 240-323 with bench_paged_kv.py's
+    defaults): per case, a cache of 64 blocks of 16 slots, K/V from N(0,1),
+    slots a random permutation of the cache with every 11th slot -1, a random
+    block table; a bit-exact gate against the torch restatement, then p50 of
+    per-call event timings back to back, for the hip backend and the torch
+    restatement.  Effective bytes are the reference's (payload x 4 for store,
+    x 2 for gather)."""
+    import numpy as np
+    import torch
+
+    from nanokv.benchmark import effective_bytes, linear_percentile
+
+    m = REFERENCE_MATRIX
+    iterations = iterations or m["iterations"]
+    ref = torch_reference_backend()
+    dtypes = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+    words = {torch.float16: torch.int16, torch.bfloat16: torch.int16}
+    records = []
+    for op in m["operations"]:
+        for dtype_name in m["dtypes"]:
+            dtype = dtypes[dtype_name]
+            for heads, dim in m["kv_shapes"]:
+                for tokens in m["tokens"]:
+                    g = torch.Generator(device=device).manual_seed(m["seed"])
+                    shape = (m["num_blocks"], m["block_size"], heads, dim)
+                    kc = torch.empty(shape, dtype=dtype, device=device).normal_(generator=g)
+                    vc = torch.empty_like(kc).normal_(generator=g)
+                    key = torch.randn((tokens, heads, dim), dtype=dtype, device=device, generator=g)
+                    value = torch.randn_like(key)
+                    capacity = m["num_blocks"] * m["block_size"]
+                    slots = torch.randperm(capacity, dtype=torch.int32, device=device,
+                                           generator=g)[:tokens].contiguous()
+                    slots[::11] = -1
+                    table = torch.randperm(m["num_blocks"], dtype=torch.int32, device=device,
+                                           generator=g)
+                    if op == "store":
+                        ek, ev = kc.clone(), vc.clone()
+                        ref.store(key, value, ek, ev, slots)
+                        backend.store(key, value, kc, vc, slots)
+                        torch.cuda.synchronize()
+                        exact = (torch.equal(kc.view(words[dtype]), ek.view(words[dtype]))
+                                 and torch.equal(vc.view(words[dtype]), ev.view(words[dtype])))
+                        calls = {"hip": lambda: backend.store(key, value, kc, vc, slots),
+                                 "torch_reference": lambda: ref.store(key, value, kc, vc, slots)}
+                    else:
+                        expect = ref.gather(kc, table, tokens)
+                        got = backend.gather(kc, table, tokens)
+                        torch.cuda.synchronize()
+                        exact = torch.equal(got.view(words[dtype]), expect.view(words[dtype]))
+                        calls = {"hip": lambda: backend.gather(kc, table, tokens),
+                                 "torch_reference": lambda: ref.gather(kc, table, tokens)}
+                    if not exact:
+                        raise AssertionError(f"hip {op} differs from the torch reference "
+                                             f"({dtype_name}, {heads}x{dim}, {tokens} tokens)")
+                    nbytes = effective_bytes(op, tokens, heads, dim, kc.element_size())
+                    record = {"operation": op, "dtype": dtype_name, "tokens": tokens,
+                              "kv_shape": f"{heads}x{dim}", "effective_bytes": nbytes}
+                    for name, call in calls.items():
+                        for _ in range(m["warmup"]):
+                            call()
+                        torch.cuda.synchronize()
+                        pairs = [(torch.cuda.Event(enable_timing=True),
+                                  torch.cuda.Event(enable_timing=True)) for _ in range(iterations)]
+                        for start, end in pairs:
+                            start.record()
+                            call()
+                            end.record()
+                        pairs[-1][1].synchronize()
+                        p50 = linear_percentile([a.elapsed_time(b) * 1e3 for a, b in pairs], 0.5)
+                        record[f"{name}_p50_us"] = round(p50, 3)
+                        record[f"{name}_gbps"] = round(nbytes / (p50 * 1e3), 3)
+                    records.append(record)
+    ratios = [r["torch_reference_p50_us"] / r["hip_p50_us"] for r in records]
+    return {"cases": records, "geomean_speedup_of_hip": round(float(np.exp(np.mean(np.log(ratios)))), 3),
+            "iterations": iterations, "warmup": m["warmup"]}
 
 
 def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer) -> dict:

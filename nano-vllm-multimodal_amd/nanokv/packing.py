@@ -24,6 +24,7 @@ import numpy as np
 import torch
 
 from nanokv import _lib
+from nanokv.paged_kv.ops import current_stream_handle
 
 
 @dataclass(slots=True)
@@ -216,7 +217,7 @@ class DevicePacker:
         return views
 
     def _stream(self) -> int:
-        return torch.cuda.current_stream(self.device).cuda_stream
+        return current_stream_handle(self.device)
 
     @staticmethod
     def _width(batch: SequenceBatch, table_width: int | None) -> int:

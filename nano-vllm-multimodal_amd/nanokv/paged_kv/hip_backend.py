@@ -3,9 +3,12 @@
 library for MI355X.
 
 It mirrors the reference's CUDA backend (nanovllm/layers/paged_kv/
-cuda_backend.py:31-104): validate with the shared validators, then call the
-``nanovllm_paged_kv`` ops.  Loading is lazy and lock-protected; a missing
-library raises instead of falling back to another backend.
+cuda_backend.py:31-104): validate with the shared validators, then run the
+``nanovllm_paged_kv`` ops.  Loading registers the ops on the CUDA key (for
+``torch.ops.nanovllm_paged_kv.*`` callers); the backend itself calls the
+same implementations directly, without the dispatcher hop.  Loading is lazy
+and lock-protected; a missing library raises instead of falling back to
+another backend.
 """
 from __future__ import annotations
 
@@ -104,7 +107,7 @@ class HIPPagedKVBackend:
         if not key.is_cuda:
             raise ValueError("HIP Paged KV Store requires ROCm device tensors")
         self._load()
-        torch.ops.nanovllm_paged_kv.store(key, value, key_cache, value_cache, slot_mapping)
+        ops.store(key, value, key_cache, value_cache, slot_mapping)
 
     def gather(
         self,
@@ -116,7 +119,7 @@ class HIPPagedKVBackend:
         if not cache.is_cuda:
             raise ValueError("HIP Paged KV Gather requires ROCm device tensors")
         self._load()
-        return torch.ops.nanovllm_paged_kv.gather(cache, block_table, sequence_length)
+        return ops.gather(cache, block_table, sequence_length)
 
     def gather_varlen(
         self,
@@ -139,7 +142,7 @@ class HIPPagedKVBackend:
         validate_varlen_inputs(key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens)
         self._load()
         if plan is None and out is None:
-            return torch.ops.nanovllm_paged_kv.gather_varlen(
+            return ops.gather_varlen(
                 key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens
             )
         if plan is None:
@@ -152,7 +155,7 @@ class HIPPagedKVBackend:
         key_out, value_out = out
         if key_out.shape[0] < total_tokens or value_out.shape != key_out.shape:
             raise ValueError("varlen Gather outputs must hold total_tokens rows")
-        torch.ops.nanovllm_paged_kv.gather_varlen_planned(
+        ops.gather_varlen_planned(
             key_cache, value_cache, plan, key_out, value_out
         )
         return key_out, value_out
@@ -168,7 +171,7 @@ class HIPPagedKVBackend:
         the shape and dtype of ``cache`` (all layers, K and V)."""
         self._load()
         num_blocks, block_size, heads, head_dim = cache.shape
-        return torch.ops.nanovllm_paged_kv.build_gather_plan(
+        return ops.build_gather_plan(
             block_tables, cu_seqlens_k, total_tokens, num_blocks, block_size,
             heads * head_dim, cache.dtype,
         )
@@ -185,7 +188,7 @@ class HIPPagedKVBackend:
         depends on the context lengths only, so one plan serves every layer
         of a step (and every step with the same lengths)."""
         self._load()
-        return torch.ops.nanovllm_paged_kv.build_attention_plan(
+        return ops.build_attention_plan(
             cu_seqlens_k, total_tokens, cache.shape[1]
         )
 
@@ -219,7 +222,7 @@ class HIPPagedKVBackend:
             plan = self.build_attention_plan(key_cache, cu_seqlens_k, total_tokens)
         if out is None:
             out = torch.empty_like(q)
-        torch.ops.nanovllm_paged_kv.paged_attention_decode(
+        ops.paged_attention_decode(
             q, key_cache, value_cache, block_tables, plan[0], plan[1], float(softmax_scale), out
         )
         return out

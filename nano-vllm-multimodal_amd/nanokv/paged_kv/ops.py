@@ -77,8 +77,20 @@ def dtype_code(dtype: torch.dtype) -> int:
         ) from None
 
 
-def _stream(device: torch.device) -> int:
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_handle(device: torch.device) -> int:
+    """The current stream of ``device`` as a hipStream_t integer: torch's raw
+    accessor when it exists (no Stream object per launch, ~0.1 us against
+    ~2 us), the public Stream object otherwise."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_stream = current_stream_handle
 
 
 def _require_device(what: str, *tensors: torch.Tensor) -> torch.device:
@@ -304,3 +316,15 @@ def register_ops() -> None:
         fragment.impl("build_attention_plan", _build_attention_plan_impl, "CUDA")
         fragment.impl("paged_attention_decode", _paged_attention_decode_impl, "CUDA")
         _FRAGMENT = fragment
+
+
+# The backend object calls the implementations directly: the registered ops
+# dispatch to these same functions, and skipping the dispatcher hop saves
+# ~1.4 us of host time per call.
+store = _store_impl
+gather = _gather_impl
+gather_varlen = _gather_varlen_impl
+build_gather_plan = _build_plan_impl
+gather_varlen_planned = _gather_planned_impl
+build_attention_plan = _build_attention_plan_impl
+paged_attention_decode = _paged_attention_decode_impl

@@ -20,6 +20,7 @@ import numpy as np
 import torch
 
 from nanokv import _lib
+from nanokv.paged_kv.ops import current_stream_handle
 
 
 class DeviceBlockPool:
@@ -69,7 +70,7 @@ class DeviceBlockPool:
 
     # -------------------------------------------------------------- control
     def _stream(self) -> int:
-        return torch.cuda.current_stream(self.device).cuda_stream
+        return current_stream_handle(self.device)
 
     @property
     def desc(self) -> _lib.PoolDesc:

@@ -80,6 +80,33 @@ def test_fused_qkv_strided_key_seed29(backend, gpu_device):
     np.testing.assert_array_equal(words(vc), hv)
 
 
+def test_registered_ops_dispatch_to_hip(backend, gpu_device):
+    """paged_kv.cpp:199-203: callers of torch.ops.nanovllm_paged_kv.store /
+    gather / gather_varlen (rather than the backend object) reach the same
+    kernels through the schemas registered on the CUDA key."""
+    torch.manual_seed(41)
+    backend._load()  # loads the library and registers the ops
+    key = torch.randn(9, 2, 64, device=gpu_device, dtype=torch.bfloat16)
+    value = torch.randn_like(key)
+    slots = torch.tensor([0, 17, -1, 4, 31, 8, 23, 2, 15], device=gpu_device, dtype=torch.int32)
+    kc = torch.full((4, 8, 2, 64), -3, device=gpu_device, dtype=torch.bfloat16)
+    vc = torch.full_like(kc, -3)
+    hk, hv = oracle_store(key, value, kc, vc, slots)
+    torch.ops.nanovllm_paged_kv.store(key, value, kc, vc, slots)
+    np.testing.assert_array_equal(words(kc), hk)
+    np.testing.assert_array_equal(words(vc), hv)
+    table = torch.tensor([3, 1, 0], device=gpu_device, dtype=torch.int32)
+    np.testing.assert_array_equal(words(torch.ops.nanovllm_paged_kv.gather(kc, table, 19)),
+                                  oracle.gather(hk, np.array([3, 1, 0]), 19))
+    tables = torch.tensor([[3, 1, 0], [2, -1, -1]], device=gpu_device, dtype=torch.int32)
+    cu = torch.tensor([0, 19, 24], device=gpu_device, dtype=torch.int32)
+    k_out, v_out = torch.ops.nanovllm_paged_kv.gather_varlen(kc, vc, tables, cu, 24)
+    expect_k = np.concatenate([oracle.gather(hk, np.array([3, 1, 0]), 19), oracle.gather(hk, np.array([2]), 5)])
+    expect_v = np.concatenate([oracle.gather(hv, np.array([3, 1, 0]), 19), oracle.gather(hv, np.array([2]), 5)])
+    np.testing.assert_array_equal(words(k_out), expect_k)
+    np.testing.assert_array_equal(words(v_out), expect_v)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_legacy_store_kvcache_on_fused_qkv(gpu_device, dtype):
     """attention.py:10-33 / :86-93: the layer's fallback store when no
