@@ -94,11 +94,11 @@ _stream = current_stream_handle
 
 
 def _require_device(what: str, *tensors: torch.Tensor) -> torch.device:
-    device = tensors[0].device
+    index = tensors[0].get_device()  # -1 for host tensors
     for tensor in tensors:
-        if not tensor.is_cuda or tensor.device != device:
+        if tensor.get_device() != index or not tensor.is_cuda:
             raise ValueError(f"{what} requires ROCm device tensors on one device")
-    return device
+    return tensors[0].device
 
 
 def _require_contiguous_cache(what: str, *caches: torch.Tensor) -> None:
