@@ -284,6 +284,49 @@ int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
                                void* out, int64_t out_seq_stride, void* stream);
 
 /*
+ * Paged-attention prefill: causal attention of each sequence's chunk of
+ * query tokens over its context, read straight from the paged cache
+ * (head_dim 128, bfloat16, query heads per kv head G = 1, 2, 4 or 8).
+ * Request i has query rows [cu_seqlens_q[i], cu_seqlens_q[i+1]) (Lq) and
+ * context rows [0, Lk), Lk = cu_seqlens_k[i+1] - cu_seqlens_k[i] >= Lq;
+ * query j sees keys [0, Lk - Lq + j]; query head h reads kv head h / G.
+ *
+ * Replaces: the prefill call flash_attn_varlen_func(q, k_cache, v_cache,
+ *   cu_seqlens_q, cu_seqlens_k, ..., causal=True, block_table=...) of
+ *   Attention.forward (nanovllm/layers/attention.py:95-116); numerics of
+ *   SDPAAttention's prefill (attention.py:226-282: per-request gather, then
+ *   SDPA with the prefix-causal mask of :155-161).
+ *
+ * nkv_build_prefill_plan cuts every request's queries into tiles of
+ *   nkv_prefill_tile_tokens(G) tokens (128 / G) and writes one int4
+ *   {seq, token0, tokens, 0} per tile into `plan` (capacity >=
+ *   nkv_prefill_plan_capacity(total query tokens, num_seqs, G)).  It reads
+ *   only cu_seqlens_q, so one plan serves every layer of a step.
+ * nkv_paged_attention_prefill runs one workgroup per (tile, kv head);
+ *   block_tables [num_seqs, table_stride] (int32, -1 padded); a block id
+ *   outside [0, num_blocks) or a row past the table drops its keys.  q and
+ *   out are [total query tokens, num_q_heads, head_dim] with token strides
+ *   q_token_stride / out_token_stride elements (q rows 16-byte aligned,
+ *   out rows 8-byte aligned).  Needs no workspace.
+ */
+int64_t nkv_prefill_tile_tokens(int64_t group);
+int64_t nkv_prefill_plan_capacity(int64_t total_q_tokens, int64_t num_seqs,
+                                  int64_t group);
+int nkv_build_prefill_plan(const int32_t* cu_seqlens_q, int64_t num_seqs,
+                           int64_t group, void* plan, int64_t capacity,
+                           void* stream);
+int nkv_paged_attention_prefill(const void* q, int64_t q_token_stride,
+                                const void* key_cache, const void* value_cache,
+                                const int32_t* block_tables, int64_t table_stride,
+                                const int32_t* cu_seqlens_q,
+                                const int32_t* cu_seqlens_k, const void* plan,
+                                int64_t capacity, int64_t num_seqs,
+                                int64_t num_kv_heads, int64_t num_q_heads,
+                                int64_t head_dim, int64_t block_size,
+                                int64_t num_blocks, float scale, int32_t dtype,
+                                void* out, int64_t out_token_stride, void* stream);
+
+/*
  * Host-to-device transfer lane: a non-blocking transfer stream (default
  * priority) and recycled events owned by the library.
  *   nkv_transfer_h2d   copies `bytes` from pinned host `src` to device `dst`

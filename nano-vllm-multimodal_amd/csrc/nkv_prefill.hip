@@ -1,0 +1,449 @@
+// Paged-attention prefill: causal attention of a chunk of query tokens per
+// sequence over that sequence's context, read straight from the paged KV
+// cache through its block table.  This is the prefill call of the
+// reference's Flash path (flash_attn_varlen_func(q, k_cache, v_cache,
+// cu_seqlens_q, cu_seqlens_k, ..., causal=True, block_table=...),
+// nanovllm/layers/attention.py:95-116); its numerical reference is the SDPA
+// prefill (attention.py:226-282: gather each request's keys, then SDPA with
+// the prefix-causal mask of :155-161).  Query j of a request with Lq queries
+// and Lk context rows sits at position Lk - Lq + j and sees keys
+// [0, Lk - Lq + j]; query head h reads kv head h / (Hq / Hkv).
+//
+// The work is GEMM-shaped (each K/V tile serves 128 query rows), so both
+// products run on MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation):
+//   * a workgroup owns 128 query rows of one (sequence, kv head): the
+//     (token, query head) pairs of 128 / G consecutive tokens and the
+//     G = Hq / Hkv query heads that share the kv head, token-major;
+//     each of its 4 waves owns 32 of those rows (two 16-row blocks);
+//   * the keys stream in tiles of 64: K is staged in LDS row-major, V
+//     transposed (4 x 8 blocks transposed in registers, then 8-byte LDS
+//     stores), both with padded rows;
+//   * scores are computed transposed, S^T = K Q^T, so that a lane's
+//     accumulators all belong to ONE query row: the online softmax needs
+//     only a 4-lane max per row, the P^T operand of O^T = V^T P^T comes
+//     straight from the score registers (the key order inside each 32-key
+//     step is permuted identically in V^T), and the output rescale is a
+//     per-lane factor;
+//   * P is rounded to bf16 for the second product, as flash attention does.
+// Invalid block ids (outside [0, num_blocks), or past the table) drop their
+// keys, as in the decode kernel.
+#include <cmath>
+
+#include "nkv_common.h"
+
+namespace nkv {
+namespace {
+
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = kPfWaves * kWave;
+constexpr int kPfRows = kPfWaves * 32;  // query rows per workgroup
+constexpr int kPfKeys = 64;             // keys per tile
+constexpr int kPfDim = 128;             // head_dim
+constexpr int kPfPlanThreads = 1024;
+// LDS row pitches in bf16 elements (padding spreads the 16 rows that one
+// MFMA operand load touches over different banks).
+constexpr int kKPitch = kPfDim + 8;   // K tile [key][d]: 272 B per key
+constexpr int kVPitch = kPfKeys + 8;  // V^T tile [d][key]: 144 B per d
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct PrefillShared {
+  uint16_t k[kPfKeys * kKPitch];
+  uint16_t vt[kPfDim * kVPitch];
+  int32_t valid[kPfKeys];
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays a quiet NaN).
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return bf16_bits(lo) | (bf16_bits(hi) << 16);
+}
+
+// Low / high 16-bit halves of two words, packed: {a.lo, b.lo} or {a.hi, b.hi}.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// Plan: one int4 {seq, token0, tokens, 0} per workgroup: tokens [token0,
+// token0 + tokens) of sequence seq's queries, tokens <= tile_tokens.
+// Entries past the total get tokens = 0.
+__global__ __launch_bounds__(kPfPlanThreads) void prefill_plan_kernel(
+    const int32_t* __restrict__ cu_seqlens_q, int32_t num_seqs, int32_t tile_tokens,
+    int4* __restrict__ plan, int64_t capacity) {
+  extern __shared__ int32_t s_mem[];
+  int32_t* s_first = s_mem;               // [num_seqs + 1]
+  int32_t* s_tmp = s_mem + num_seqs + 1;  // [kPfPlanThreads / 64 + 1]
+  lds_exclusive_scan<kPfPlanThreads>(
+      num_seqs,
+      [&](int32_t i) {
+        const int32_t len = cu_seqlens_q[i + 1] - cu_seqlens_q[i];
+        return len > 0 ? (len + tile_tokens - 1) / tile_tokens : 0;
+      },
+      s_first, s_tmp);
+  const int64_t total = s_first[num_seqs];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kPfPlanThreads;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kPfPlanThreads + threadIdx.x; e < capacity;
+       e += stride) {
+    int4 entry = make_int4(0, 0, 0, 0);
+    if (e < total) {
+      const int32_t i = owner_of(s_first, num_seqs, static_cast<int32_t>(e));
+      const int32_t t0 = (static_cast<int32_t>(e) - s_first[i]) * tile_tokens;
+      const int32_t len = cu_seqlens_q[i + 1] - cu_seqlens_q[i];
+      entry = make_int4(i, t0, min(tile_tokens, len - t0), 0);
+    }
+    plan[e] = entry;
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
+    const uint16_t* __restrict__ q, int64_t q_token_stride,
+    const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
+    const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,
+    int32_t num_blocks, int32_t num_kv_heads, const int32_t* __restrict__ cu_seqlens_q,
+    const int32_t* __restrict__ cu_seqlens_k, const int4* __restrict__ plan, int32_t num_seqs,
+    float scale_log2, uint16_t* __restrict__ out, int64_t out_token_stride) {
+  constexpr int kTileTokens = kPfRows / G;
+  __shared__ PrefillShared sh;
+
+  const int4 entry = plan[blockIdx.x];
+  const int32_t seq = entry.x;
+  const int32_t tok0 = entry.y;
+  const int32_t ntok = entry.z;
+  const int32_t kh = blockIdx.y;
+  // Uniform exits for empty or malformed entries.
+  if (ntok <= 0 || ntok > kTileTokens || seq < 0 || seq >= num_seqs || tok0 < 0) return;
+  const int32_t q_begin = cu_seqlens_q[seq];
+  const int32_t lq = cu_seqlens_q[seq + 1] - q_begin;
+  const int32_t lk = cu_seqlens_k[seq + 1] - cu_seqlens_k[seq];
+  if (lk < lq || tok0 + ntok > lq) return;
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int c16 = lane & 15;  // the lane's query row inside a 16-row block
+  const int g4 = lane >> 4;   // which quarter of the MFMA k dimension the lane holds
+  const int64_t row_bytes = static_cast<int64_t>(num_kv_heads) * kPfDim * 2;
+  const int32_t* table = tables + static_cast<int64_t>(seq) * table_stride;
+
+  // Q^T operands (B of S^T = K Q^T): lane holds row m, dims 32 * dc + 8 * g4 .. +8.
+  bf16x8 qb[2][4];
+  int32_t limit[2];  // last visible key of the lane's row, -1 for rows past the tile
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    const int m = wave * 32 + mb * 16 + c16;
+    const int t = m / G;
+    const bool row_ok = t < ntok;
+    limit[mb] = row_ok ? lk - lq + tok0 + t : -1;
+    const uint16_t* qrow = q + static_cast<int64_t>(q_begin + tok0 + (row_ok ? t : 0)) *
+                                   q_token_stride + (kh * G + m % G) * kPfDim;
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row_ok) v = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * g4);
+      qb[mb][dc] = as_bf16x8(v);
+    }
+  }
+
+  const int32_t num_keys = lk - lq + tok0 + ntok;  // keys the last row sees, <= lk
+  const int32_t num_tiles = (num_keys + kPfKeys - 1) / kPfKeys;
+  float row_max[2] = {-INFINITY, -INFINITY};
+  float row_sum[2] = {0.f, 0.f};  // this lane's share of the row's weight sum
+  f32x4 acc[8][2];                // O^T blocks: dims 16 * db + 4 * g4 + i, row m
+#pragma unroll
+  for (int db = 0; db < 8; ++db) {
+    acc[db][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int32_t tile = 0; tile < num_tiles; ++tile) {
+    const int32_t key0 = tile * kPfKeys;
+    __syncthreads();  // the previous tile's LDS reads are done
+    // K tile: 64 keys x 16 words of 16 B, 4 words per thread, row-major.
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int idx = w * kPfThreads + tid;
+      const int key = idx >> 4;
+      const int dch = idx & 15;
+      const int32_t t = key0 + key;
+      const int32_t logical = t / block_size;
+      int32_t block = -1;
+      if (t < num_keys && logical < table_stride) block = table[logical];
+      const bool ok = block >= 0 && block < num_blocks;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (ok) {
+        const int64_t row = static_cast<int64_t>(block) * block_size + t % block_size;
+        v = reinterpret_cast<const u32x4*>(key_cache + row * row_bytes + kh * kPfDim * 2)[dch];
+      }
+      *reinterpret_cast<u32x4*>(&sh.k[key * kKPitch + dch * 8]) = v;
+      if (dch == 0) sh.valid[key] = ok ? 1 : 0;
+    }
+    // V tile transposed: thread -> 4 keys x 8 dims, stored as 8 rows of 4 keys.
+    {
+      const int kq = tid >> 4;  // keys 4 * kq .. +4
+      const int dq = tid & 15;  // dims 8 * dq .. +8
+      u32x4 r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int32_t t = key0 + 4 * kq + j;
+        const int32_t logical = t / block_size;
+        int32_t block = -1;
+        if (t < num_keys && logical < table_stride) block = table[logical];
+        r[j] = u32x4{0u, 0u, 0u, 0u};
+        if (block >= 0 && block < num_blocks) {
+          const int64_t row = static_cast<int64_t>(block) * block_size + t % block_size;
+          r[j] = reinterpret_cast<const u32x4*>(value_cache + row * row_bytes +
+                                                 kh * kPfDim * 2)[dq];
+        }
+      }
+      const uint32_t w0[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+      const uint32_t w1[4] = {r[1].x, r[1].y, r[1].z, r[1].w};
+      const uint32_t w2[4] = {r[2].x, r[2].y, r[2].z, r[2].w};
+      const uint32_t w3[4] = {r[3].x, r[3].y, r[3].z, r[3].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {  // dims 2c (low halves) and 2c + 1 (high halves)
+        const u32x2 even = {pack_lo(w0[c], w1[c]), pack_lo(w2[c], w3[c])};
+        const u32x2 odd = {pack_hi(w0[c], w1[c]), pack_hi(w2[c], w3[c])};
+        *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c) * kVPitch + 4 * kq]) = even;
+        *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c + 1) * kVPitch + 4 * kq]) = odd;
+      }
+    }
+    __syncthreads();
+
+    // S^T = K Q^T: block (kb, mb) holds keys 16 kb + 4 g4 + i of row m.
+    f32x4 st[4][2];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      st[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      st[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dc = 0; dc < 4; ++dc) {
+        const bf16x8 a = as_bf16x8(
+            *reinterpret_cast<const u32x4*>(&sh.k[(16 * kb + c16) * kKPitch + 32 * dc + 8 * g4]));
+        st[kb][0] = mfma(a, qb[0][dc], st[kb][0]);
+        st[kb][1] = mfma(a, qb[1][dc], st[kb][1]);
+      }
+    }
+
+    // Online softmax per row (exp2 units); P^T operands for both 32-key steps.
+    bf16x8 pb[2][2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      float s[4][4];
+      float local = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = 16 * kb + 4 * g4 + i;
+          const bool visible = key0 + key <= limit[mb] && sh.valid[key] != 0;
+          s[kb][i] = visible ? st[kb][mb][i] * scale_log2 : -INFINITY;
+          local = fmaxf(local, s[kb][i]);
+        }
+      }
+      local = fmaxf(local, __shfl_xor(local, 16, kWave));
+      local = fmaxf(local, __shfl_xor(local, 32, kWave));
+      const float m_new = fmaxf(row_max[mb], local);
+      float p[4][4];
+      float psum = 0.f;
+      if (m_new == -INFINITY) {  // nothing visible yet in this row
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[kb][i] = 0.f;
+      } else {
+        const float alpha = __builtin_amdgcn_exp2f(row_max[mb] - m_new);  // 0 when row_max is -inf
+        row_sum[mb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) acc[db][mb] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            p[kb][i] = __builtin_amdgcn_exp2f(s[kb][i] - m_new);  // exp2(-inf) = 0 for hidden keys
+            psum += p[kb][i];
+          }
+        row_max[mb] = m_new;
+      }
+      row_sum[mb] += psum;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x4 w = {pack_bf16(p[2 * c][0], p[2 * c][1]), pack_bf16(p[2 * c][2], p[2 * c][3]),
+                         pack_bf16(p[2 * c + 1][0], p[2 * c + 1][1]),
+                         pack_bf16(p[2 * c + 1][2], p[2 * c + 1][3])};
+        pb[c][mb] = as_bf16x8(w);
+      }
+    }
+
+    // O^T += V^T P^T.  Step c covers keys 32 c .. +32 in the order the P^T
+    // operand holds them: slots 0-3 = keys 32c + 4 g4 + j, slots 4-7 = keys
+    // 32c + 16 + 4 g4 + j.
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const uint16_t* vrow = &sh.vt[(16 * db + c16) * kVPitch];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 32 * c + 4 * g4);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 32 * c + 16 + 4 * g4);
+        const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
+        acc[db][0] = mfma(a, pb[c][0], acc[db][0]);
+        acc[db][1] = mfma(a, pb[c][1], acc[db][1]);
+      }
+    }
+  }
+
+  // Normalise and store: the row's weight sum is spread over its 4 lanes.
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    float total = row_sum[mb];
+    total += __shfl_xor(total, 16, kWave);
+    total += __shfl_xor(total, 32, kWave);
+    const int m = wave * 32 + mb * 16 + c16;
+    const int t = m / G;
+    if (t >= ntok) continue;
+    const float inv = total > 0.f ? 1.f / total : 0.f;
+    uint16_t* orow = out + static_cast<int64_t>(q_begin + tok0 + t) * out_token_stride +
+                     (kh * G + m % G) * kPfDim;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const f32x4 v = acc[db][mb];
+      const u32x2 w = {pack_bf16(v.x * inv, v.y * inv), pack_bf16(v.z * inv, v.w * inv)};
+      *reinterpret_cast<u32x2*>(orow + 16 * db + 4 * g4) = w;
+    }
+  }
+}
+
+using PrefillKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const uint8_t*,
+                               const int32_t*, int64_t, int32_t, int32_t, int32_t,
+                               const int32_t*, const int32_t*, const int4*, int32_t, float,
+                               uint16_t*, int64_t);
+
+PrefillKernel prefill_kernel_for(int64_t group) {
+  switch (group) {
+    case 1: return attn_prefill_kernel<1>;
+    case 2: return attn_prefill_kernel<2>;
+    case 4: return attn_prefill_kernel<4>;
+    case 8: return attn_prefill_kernel<8>;
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+}  // namespace nkv
+
+extern "C" int64_t nkv_prefill_tile_tokens(int64_t group) {
+  return group == 1 || group == 2 || group == 4 || group == 8 ? nkv::kPfRows / group : 0;
+}
+
+extern "C" int64_t nkv_prefill_plan_capacity(int64_t total_q_tokens, int64_t num_seqs,
+                                             int64_t group) {
+  const int64_t tile = nkv_prefill_tile_tokens(group);
+  if (total_q_tokens < 0 || num_seqs < 0 || tile == 0) return 0;
+  return (total_q_tokens + tile - 1) / tile + num_seqs;
+}
+
+extern "C" int nkv_build_prefill_plan(const int32_t* cu_seqlens_q, int64_t num_seqs,
+                                      int64_t group, void* plan, int64_t capacity, void* stream) {
+  using namespace nkv;
+  const int64_t tile = nkv_prefill_tile_tokens(group);
+  if (tile == 0) {
+    return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: query heads per kv head must be "
+                                   "1, 2, 4 or 8 (got %lld)", static_cast<long long>(group));
+  }
+  if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX) {
+    return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: num_seqs=%lld or capacity=%lld "
+                                   "out of range", static_cast<long long>(num_seqs),
+                    static_cast<long long>(capacity));
+  }
+  if (capacity == 0) return NKV_OK;
+  if (!plan || (num_seqs > 0 && !cu_seqlens_q)) {
+    return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: null pointer");
+  }
+  if (reinterpret_cast<uint64_t>(plan) % 16 != 0) {
+    return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: plan must be 16-byte aligned");
+  }
+  const int64_t blocks = (capacity + kPfPlanThreads - 1) / kPfPlanThreads;
+  const size_t lds = (static_cast<size_t>(num_seqs) + 1 + kPfPlanThreads / kWave + 1) *
+                     sizeof(int32_t);
+  prefill_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPfPlanThreads), lds,
+                        static_cast<hipStream_t>(stream)>>>(
+      cu_seqlens_q, static_cast<int32_t>(num_seqs), static_cast<int32_t>(tile),
+      static_cast<int4*>(plan), capacity);
+  return nkv_check_launch("nkv_build_prefill_plan");
+}
+
+extern "C" int nkv_paged_attention_prefill(
+    const void* q, int64_t q_token_stride, const void* key_cache, const void* value_cache,
+    const int32_t* block_tables, int64_t table_stride, const int32_t* cu_seqlens_q,
+    const int32_t* cu_seqlens_k, const void* plan, int64_t capacity, int64_t num_seqs,
+    int64_t num_kv_heads, int64_t num_q_heads, int64_t head_dim, int64_t block_size,
+    int64_t num_blocks, float scale, int32_t dtype, void* out, int64_t out_token_stride,
+    void* stream) {
+  using namespace nkv;
+  if (dtype != NKV_DTYPE_BFLOAT16) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: only bfloat16 is supported");
+  }
+  if (head_dim != kPfDim) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: head_dim must be %d", kPfDim);
+  }
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      num_kv_heads > 65535) {
+    return nkv_fail(NKV_E_INVALID,
+                    "nkv_paged_attention_prefill: num_q_heads must be a multiple of num_kv_heads");
+  }
+  const PrefillKernel kernel = prefill_kernel_for(num_q_heads / num_kv_heads);
+  if (kernel == nullptr) {
+    return nkv_fail(NKV_E_INVALID,
+                    "nkv_paged_attention_prefill: %lld query heads per kv head (1, 2, 4 or 8 "
+                    "supported)", static_cast<long long>(num_q_heads / num_kv_heads));
+  }
+  if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX ||
+      block_size <= 0 || num_blocks < 0 || num_blocks * block_size > INT32_MAX ||
+      table_stride < 0 || q_token_stride < num_q_heads * head_dim ||
+      out_token_stride < num_q_heads * head_dim) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: bad sizes or strides");
+  }
+  if (!std::isfinite(scale)) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: scale must be finite");
+  }
+  if (num_seqs == 0 || capacity == 0) return NKV_OK;
+  if (!q || !key_cache || !value_cache || !out || !plan || !cu_seqlens_q || !cu_seqlens_k ||
+      (table_stride > 0 && !block_tables)) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: null pointer");
+  }
+  if ((reinterpret_cast<uint64_t>(q) | reinterpret_cast<uint64_t>(key_cache) |
+       reinterpret_cast<uint64_t>(value_cache) | reinterpret_cast<uint64_t>(plan) |
+       static_cast<uint64_t>(q_token_stride * 2)) % 16 != 0 ||
+      (reinterpret_cast<uint64_t>(out) | static_cast<uint64_t>(out_token_stride * 2)) % 8 != 0) {
+    return nkv_fail(NKV_E_INVALID,
+                    "nkv_paged_attention_prefill: q/caches/plan must be 16-byte aligned and out "
+                    "rows 8-byte aligned");
+  }
+  const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
+  kernel<<<dim3(static_cast<unsigned>(capacity), static_cast<unsigned>(num_kv_heads)),
+           dim3(kPfThreads), 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(q), q_token_stride, static_cast<const uint8_t*>(key_cache),
+      static_cast<const uint8_t*>(value_cache), block_tables, table_stride,
+      static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
+      static_cast<int32_t>(num_kv_heads), cu_seqlens_q, cu_seqlens_k,
+      static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2,
+      static_cast<uint16_t*>(out), out_token_stride);
+  return nkv_check_launch("nkv_paged_attention_prefill");
+}

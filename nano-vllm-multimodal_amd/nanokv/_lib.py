@@ -90,6 +90,16 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
             c_ptr,
         ),
     ),
+    "nkv_prefill_tile_tokens": (c_i64, (c_i64,)),
+    "nkv_prefill_plan_capacity": (c_i64, (c_i64, c_i64, c_i64)),
+    "nkv_build_prefill_plan": (ctypes.c_int, (c_ptr, c_i64, c_i64, c_ptr, c_i64, c_ptr)),
+    "nkv_paged_attention_prefill": (
+        ctypes.c_int,
+        (
+            c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_i64,
+            c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_float, c_i32, c_ptr, c_i64, c_ptr,
+        ),
+    ),
     "nkv_transfer_create": (ctypes.c_int, (c_i32, c_ptr_out)),
     "nkv_transfer_destroy": (ctypes.c_int, (c_ptr,)),
     "nkv_transfer_h2d": (ctypes.c_int, (c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64_out)),

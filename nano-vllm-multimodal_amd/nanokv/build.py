@@ -25,6 +25,7 @@ SOURCES = (
     "nkv_pack.hip",
     "nkv_transfer.hip",
     "nkv_attention.hip",
+    "nkv_prefill.hip",
     "nkv_pool.hip",
 )
 OFFLOAD_ARCH = "gfx950"

@@ -227,6 +227,58 @@ class HIPPagedKVBackend:
         )
         return out
 
+    def build_prefill_plan(self, q: torch.Tensor, key_cache: torch.Tensor,
+                           cu_seqlens_q: torch.Tensor) -> torch.Tensor:
+        """Query tiles for :meth:`paged_attention_prefill`; depends on
+        cu_seqlens_q and the head layout only, so one plan serves every layer
+        of a step."""
+        self._load()
+        group = q.shape[1] // key_cache.shape[2]
+        return ops.build_prefill_plan(cu_seqlens_q, q.shape[0], group)
+
+    def paged_attention_prefill(
+        self,
+        q: torch.Tensor,
+        key_cache: torch.Tensor,
+        value_cache: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_q: torch.Tensor,
+        cu_seqlens_k: torch.Tensor,
+        softmax_scale: float,
+        *,
+        total_context_tokens: int | None = None,
+        plan: torch.Tensor | None = None,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Causal prefill attention read straight from the paged caches: the
+        prefill call of Attention.forward (flash_attn_varlen_func with
+        block_table, attention.py:95-116) with the numerics of SDPAAttention's
+        prefill (attention.py:226-282).  Request i's queries are rows
+        [cu_seqlens_q[i], cu_seqlens_q[i+1]) of q [Tq, Hq, 128] bf16; its
+        context is the first Lk = cu_seqlens_k[i+1] - cu_seqlens_k[i] rows
+        of its block table, the queries being the last Lq of them.
+        ``total_context_tokens`` (= cu_seqlens_k[-1]) is only read by the
+        host-side value checks of index validation (read from the device
+        when not given)."""
+        from nanokv.paged_kv.base import index_value_validation_enabled
+
+        total = total_context_tokens
+        if total is None:  # read it only when the (synchronising) value checks run anyway
+            total = int(cu_seqlens_k[-1]) if index_value_validation_enabled(cu_seqlens_k) else 0
+        validate_varlen_inputs(key_cache, value_cache, block_tables, cu_seqlens_k, int(total))
+        if cu_seqlens_q.shape != cu_seqlens_k.shape:
+            raise ValueError("cu_seqlens_q and cu_seqlens_k must have num_seqs + 1 entries each")
+        if q.ndim != 3 or q.device != key_cache.device:
+            raise ValueError("q must be [tokens, num_q_heads, head_dim] on the caches' device")
+        self._load()
+        if plan is None:
+            plan = self.build_prefill_plan(q, key_cache, cu_seqlens_q)
+        if out is None:
+            out = torch.empty_like(q)
+        ops.paged_attention_prefill(q, key_cache, value_cache, block_tables, cu_seqlens_q,
+                                    cu_seqlens_k, plan, float(softmax_scale), out)
+        return out
+
 
 def validate_varlen_inputs(
     key_cache: torch.Tensor,

@@ -56,6 +56,11 @@ SCHEMAS = {
     "paged_attention_decode": "paged_attention_decode(Tensor q, Tensor key_cache, "
     "Tensor value_cache, Tensor block_tables, Tensor plan, Tensor first_part, float scale, "
     "Tensor(a!) out) -> ()",
+    "build_prefill_plan": "build_prefill_plan(Tensor cu_seqlens_q, int total_q_tokens, "
+    "int group) -> Tensor",
+    "paged_attention_prefill": "paged_attention_prefill(Tensor q, Tensor key_cache, "
+    "Tensor value_cache, Tensor block_tables, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
+    "Tensor plan, float scale, Tensor(a!) out) -> ()",
 }
 
 DTYPE_CODES = {
@@ -296,6 +301,61 @@ def _paged_attention_decode_impl(q, key_cache, value_cache, block_tables, plan, 
     _lib.check(status, "nanovllm_paged_kv::paged_attention_decode")
 
 
+def _require_cu(name: str, cu: torch.Tensor, num_seqs: int | None = None) -> int:
+    if cu.dtype != torch.int32 or cu.ndim != 1 or not cu.is_contiguous() or cu.numel() < 1:
+        raise ValueError(f"{name} must be a contiguous 1-D int32 tensor of num_seqs + 1 entries")
+    if num_seqs is not None and cu.numel() != num_seqs + 1:
+        raise ValueError(f"{name} must have num_seqs + 1 entries")
+    return cu.numel() - 1
+
+
+def _build_prefill_plan_impl(cu_seqlens_q, total_q_tokens: int, group: int):
+    device = _require_device("paged KV HIP prefill plan", cu_seqlens_q)
+    num_seqs = _require_cu("cu_seqlens_q", cu_seqlens_q)
+    library = _lib.load_library()
+    capacity = int(library.nkv_prefill_plan_capacity(total_q_tokens, num_seqs, group))
+    if capacity == 0 and total_q_tokens > 0:
+        raise ValueError("prefill attention supports 1, 2, 4 or 8 query heads per kv head")
+    plan = torch.empty((capacity, 4), dtype=torch.int32, device=device)
+    status = library.nkv_build_prefill_plan(
+        cu_seqlens_q.data_ptr(), num_seqs, group, plan.data_ptr() if capacity else None, capacity,
+        _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::build_prefill_plan")
+    return plan
+
+
+def _paged_attention_prefill_impl(q, key_cache, value_cache, block_tables, cu_seqlens_q,
+                                  cu_seqlens_k, plan, scale: float, out) -> None:
+    device = _require_device("paged KV HIP prefill attention", q, key_cache, value_cache,
+                             block_tables, cu_seqlens_q, cu_seqlens_k, plan, out)
+    num_seqs = _require_cu("cu_seqlens_q", cu_seqlens_q)
+    _require_cu("cu_seqlens_k", cu_seqlens_k, num_seqs)
+    if (block_tables.dtype != torch.int32 or block_tables.ndim != 2
+            or block_tables.shape[0] != num_seqs or not block_tables.is_contiguous()):
+        raise ValueError("block_tables must be a contiguous [num_seqs, width] int32 tensor")
+    _require_contiguous_cache("paged KV HIP prefill attention", key_cache, value_cache)
+    if q.dtype != torch.bfloat16 or key_cache.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
+        raise ValueError("paged attention prefill supports bfloat16 q, caches and output")
+    if q.ndim != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
+        raise ValueError("q must be [tokens, num_q_heads, head_dim] with contiguous heads")
+    if out.shape != q.shape or out.stride(2) != 1 or out.stride(1) != out.shape[2]:
+        raise ValueError("out must match q's shape with contiguous heads")
+    num_blocks, block_size, num_kv_heads, head_dim = key_cache.shape
+    if q.shape[2] != head_dim:
+        raise ValueError("q head_dim does not match the cache")
+    if plan.dtype != torch.int32 or plan.ndim != 2 or plan.shape[1] != 4 or not plan.is_contiguous():
+        raise ValueError("prefill plan must be a contiguous [capacity, 4] int32 tensor")
+    status = _lib.load_library().nkv_paged_attention_prefill(
+        q.data_ptr(), q.stride(0), key_cache.data_ptr(), value_cache.data_ptr(),
+        block_tables.data_ptr(), block_tables.shape[1], cu_seqlens_q.data_ptr(),
+        cu_seqlens_k.data_ptr(), plan.data_ptr() if plan.shape[0] else None, plan.shape[0],
+        num_seqs, num_kv_heads, q.shape[1], head_dim, block_size, num_blocks, float(scale),
+        _lib.NKV_DTYPE_BFLOAT16, out.data_ptr(), out.stride(0), _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::paged_attention_prefill")
+
+
 def register_ops() -> None:
     """Define the schemas (unless another library already did) and register
     the HIP implementations on the CUDA key.  Idempotent."""
@@ -315,6 +375,8 @@ def register_ops() -> None:
         fragment.impl("gather_varlen_planned", _gather_planned_impl, "CUDA")
         fragment.impl("build_attention_plan", _build_attention_plan_impl, "CUDA")
         fragment.impl("paged_attention_decode", _paged_attention_decode_impl, "CUDA")
+        fragment.impl("build_prefill_plan", _build_prefill_plan_impl, "CUDA")
+        fragment.impl("paged_attention_prefill", _paged_attention_prefill_impl, "CUDA")
         _FRAGMENT = fragment
 
 
@@ -328,3 +390,5 @@ build_gather_plan = _build_plan_impl
 gather_varlen_planned = _gather_planned_impl
 build_attention_plan = _build_attention_plan_impl
 paged_attention_decode = _paged_attention_decode_impl
+build_prefill_plan = _build_prefill_plan_impl
+paged_attention_prefill = _paged_attention_prefill_impl

@@ -93,6 +93,47 @@ def paged_attention_decode(q, key_cache, value_cache, block_tables, context_lens
     return out
 
 
+def paged_attention_prefill(q, cu_seqlens_q, key_cache, value_cache, block_tables, cu_seqlens_k,
+                            scale: float):
+    """Prefill attention over the paged cache in float32, as the reference's
+    prefill computes it when block tables are present: the Flash path reads
+    the cache through block_table (nanovllm/layers/attention.py:95-116,
+    flash_attn_varlen_func(..., causal=True, block_table=...)); the SDPA path
+    gathers each request's keys (:242-251) and applies the prefix-causal
+    mask (:155-161, :252-282).  Request i has query rows
+    [cu_seqlens_q[i], cu_seqlens_q[i+1]) (Lq of them) and context rows
+    [0, Lk), Lk = cu_seqlens_k[i+1] - cu_seqlens_k[i] >= Lq; its query j sits
+    at position Lk - Lq + j and attends keys [0, Lk - Lq + j].  Query head h
+    reads kv head h // (Hq / Hkv).  q [Tq, Hq, D] float32, caches bf16 words
+    [NB, BS, Hkv, D]; returns [Tq, Hq, D] float32."""
+    q = np.asarray(q, dtype=np.float32)
+    tq, hq, d = q.shape
+    hkv = key_cache.shape[2]
+    group = hq // hkv
+    cu_q = np.asarray(cu_seqlens_q).astype(np.int64)
+    cu_k = np.asarray(cu_seqlens_k).astype(np.int64)
+    out = np.zeros((tq, hq, d), dtype=np.float32)
+    for i in range(len(cu_q) - 1):
+        q0, lq = int(cu_q[i]), int(cu_q[i + 1] - cu_q[i])
+        lk = int(cu_k[i + 1] - cu_k[i])
+        if lq == 0:
+            continue
+        if lk < lq:
+            raise ValueError("every request needs at least as many keys as queries")
+        k = bf16_words_to_f32(gather(key_cache, block_tables[i], lk))
+        v = bf16_words_to_f32(gather(value_cache, block_tables[i], lk))
+        visible = np.arange(lk)[None, :] <= (lk - lq + np.arange(lq))[:, None]  # [Lq, Lk]
+        for h in range(hq):
+            kv = h // group
+            scores = (q[q0:q0 + lq, h, :] @ k[:, kv, :].T) * np.float32(scale)
+            scores = np.where(visible, scores, -np.inf)
+            scores = scores - scores.max(axis=1, keepdims=True)
+            p = np.exp(scores)
+            p /= p.sum(axis=1, keepdims=True)
+            out[q0:q0 + lq, h, :] = p @ v[:, kv, :]
+    return out
+
+
 # --------------------------------------------------------------------- packing
 
 @dataclass

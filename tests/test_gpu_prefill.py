@@ -1,0 +1,215 @@
+"""Paged-attention prefill on the GPU vs the float32 oracle
+(oracle.paged_kv.paged_attention_prefill, pinned to torch's SDPA with the
+reference's prefix-causal mask in tests/test_prefill_oracle.py).
+
+Tolerance: scores and the softmax run in fp32; the weights p are rounded to
+bf16 before the second product (as flash attention does) and the result to
+bf16 once.  Each rounding is <= 2^-9 relative, so an element differs from
+the fp32 result by at most 2^-9 * sum_k p_k |v_k| / sum_k p_k (the same
+attention over |V|, "ref_abs") plus 2^-9 * |ref|; the tests allow
+1e-3 + 2^-8 * (ref_abs + |ref|).  Which keys each query sees is checked
+exactly by test_visibility_is_exact (uniform weights, indicator values).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_kv as oracle
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def backend(gpu_device):
+    from nanokv.paged_kv import create_paged_kv_backend
+
+    return create_paged_kv_backend("hip")
+
+
+def check_close(got: torch.Tensor, ref: np.ndarray, ref_abs: np.ndarray, what: str) -> None:
+    g = got.float().cpu().numpy()
+    bad = np.abs(g - ref) > ATOL + 2.0 ** -8 * (ref_abs + np.abs(ref))
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements off, max err {np.abs(g - ref).max():.3e}"
+
+
+def build_case(device, hkv, g, bs, q_lens, k_lens, seed, q_extra_heads=0, spare_blocks=5):
+    gen = torch.Generator().manual_seed(seed)
+    b = len(q_lens)
+    need = [-(-int(n) // bs) for n in k_lens]
+    nb = sum(need) + spare_blocks
+    width = max(1, max(need))
+    perm = torch.randperm(nb, generator=gen).numpy()
+    tables = np.full((b, width), -1, np.int32)
+    cursor = 0
+    for i, n in enumerate(need):
+        tables[i, :n] = perm[cursor:cursor + n]
+        cursor += n
+    kc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16)
+    vc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16)
+    hq = hkv * g
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)]).astype(np.int32)
+    q_full = torch.randn(int(cu_q[-1]), hq + q_extra_heads, 128, generator=gen).to(torch.bfloat16)
+    dev = dict(
+        kc=kc.to(device), vc=vc.to(device), q=q_full.to(device)[:, :hq],
+        tables=torch.from_numpy(tables).to(device), cu_q=torch.from_numpy(cu_q).to(device),
+        cu_k=torch.from_numpy(cu_k).to(device),
+    )
+    host = dict(q=q_full[:, :hq].float().numpy(), kc=kc.view(torch.int16).numpy(),
+                vc=vc.view(torch.int16).numpy(), tables=tables, cu_q=cu_q, cu_k=cu_k)
+    return dev, host
+
+
+def run(backend, dev, scale, **kw):
+    return backend.paged_attention_prefill(dev["q"], dev["kc"], dev["vc"], dev["tables"],
+                                           dev["cu_q"], dev["cu_k"], scale, **kw)
+
+
+def reference(host, scale, tables=None):
+    """(fp32 attention, the same attention over |V|)."""
+    tables = host["tables"] if tables is None else tables
+    ref = oracle.paged_attention_prefill(host["q"], host["cu_q"], host["kc"], host["vc"], tables,
+                                         host["cu_k"], scale)
+    v_abs = host["vc"] & np.int16(0x7FFF)  # bf16 words with the sign cleared
+    ref_abs = oracle.paged_attention_prefill(host["q"], host["cu_q"], host["kc"], v_abs, tables,
+                                             host["cu_k"], scale)
+    return ref, ref_abs
+
+
+@pytest.mark.parametrize("hkv,g,bs", [
+    (8, 2, 256), (8, 2, 16), (2, 8, 16), (4, 4, 32), (1, 1, 16), (2, 4, 8), (8, 1, 256), (1, 8, 64),
+])
+def test_prefill_matches_oracle(backend, gpu_device, hkv, g, bs):
+    """Full prompts (Lq == Lk), continuation chunks over a cached prefix
+    (Lk > Lq), single-token chunks, chunks of several query tiles, ragged
+    last blocks, and an empty request."""
+    q_lens = [1, 37, 200, 64, 1, 0, 130]
+    k_lens = [1, 37, 333, 64 + 3 * bs + 5, 90, 12, 130]
+    dev, host = build_case(gpu_device, hkv, g, bs, q_lens, k_lens, seed=hkv * 100 + g * 10 + bs)
+    scale = 1.0 / math.sqrt(128)
+    out = run(backend, dev, scale)
+    check_close(out, *reference(host, scale), f"hkv={hkv} g={g} bs={bs}")
+
+
+def test_plan_tiles_cover_every_query(backend, gpu_device):
+    from nanokv import _lib
+
+    q_lens, k_lens = [200, 1, 0, 64, 65], [300, 5, 3, 64, 65]
+    dev, host = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=3)
+    tile = int(_lib.load_library().nkv_prefill_tile_tokens(2))
+    assert tile == 64
+    plan = backend.build_prefill_plan(dev["q"], dev["kc"], dev["cu_q"]).cpu().numpy()
+    expect = [-(-n // tile) for n in q_lens]
+    entries = plan[: sum(expect)]
+    for i, n in enumerate(q_lens):
+        own = entries[entries[:, 0] == i]
+        assert own[:, 1].tolist() == list(range(0, n, tile))
+        assert int(own[:, 2].sum()) == n
+    assert not plan[sum(expect):, 2].any()
+
+
+def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):
+    """q as a view of a wider projection (token stride > Hq * D), a plan
+    built once and reused, and a caller-provided output."""
+    q_lens, k_lens = [70, 9], [100, 9]
+    dev, host = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=7, q_extra_heads=8)
+    assert dev["q"].stride(0) == 24 * 128
+    plan = backend.build_prefill_plan(dev["q"], dev["kc"], dev["cu_q"])
+    out = torch.empty((sum(q_lens), 16, 128), dtype=torch.bfloat16, device=gpu_device)
+    ref, ref_abs = reference(host, 0.1)
+    for _ in range(2):
+        out.zero_()
+        run(backend, dev, 0.1, plan=plan, out=out)
+        check_close(out, ref, ref_abs, "planned")
+
+
+def test_invalid_block_ids_drop_their_keys(backend, gpu_device):
+    bs = 16
+    q_lens, k_lens = [20, 8], [5 * bs, 3 * bs + 4]
+    dev, host = build_case(gpu_device, 4, 2, bs, q_lens, k_lens, seed=11)
+    nb = host["kc"].shape[0]
+    bad = host["tables"].copy()
+    bad[0, 1] = nb + 7   # a prefix block out of range
+    bad[1, 0] = -1       # negative
+    out = backend.paged_attention_prefill(dev["q"], dev["kc"], dev["vc"],
+                                          torch.from_numpy(bad).to(gpu_device), dev["cu_q"],
+                                          dev["cu_k"], 1 / math.sqrt(128))
+    # expected: the same keys without the dropped blocks, positions unchanged
+    ref = np.zeros((sum(q_lens), 8, 128), np.float32)
+    ref_abs = np.zeros_like(ref)
+    k = [oracle.bf16_words_to_f32(oracle.gather(host["kc"], host["tables"][i], n)) for i, n in enumerate(k_lens)]
+    v = [oracle.bf16_words_to_f32(oracle.gather(host["vc"], host["tables"][i], n)) for i, n in enumerate(k_lens)]
+    scale = 1 / math.sqrt(128)
+    for i, (lq, lk) in enumerate(zip(q_lens, k_lens)):
+        kept = np.array([0 <= bad[i, t // bs] < nb for t in range(lk)])
+        for j in range(lq):
+            visible = kept & (np.arange(lk) <= lk - lq + j)
+            for h in range(8):
+                if not visible.any():
+                    continue
+                s = (k[i][visible, h // 2] @ host["q"][host["cu_q"][i] + j, h]) * scale
+                p = np.exp(s - s.max())
+                ref[host["cu_q"][i] + j, h] = (p / p.sum()) @ v[i][visible, h // 2]
+                ref_abs[host["cu_q"][i] + j, h] = (p / p.sum()) @ np.abs(v[i][visible, h // 2])
+    check_close(out, ref, ref_abs, "invalid blocks")
+
+
+@pytest.mark.parametrize("g,bs", [(2, 16), (1, 256), (8, 8)])
+def test_visibility_is_exact(backend, gpu_device, g, bs):
+    """q = 0 makes every visible key weigh exactly 1 (also after bf16
+    rounding), and V[t][d] = 1 when t % 128 == d, else 0: output[j][d] is
+    then the count of visible keys t with t % 128 == d over the count of
+    visible keys, which is exact in fp32.  Any key wrongly shown or hidden
+    (tile boundaries, the causal offset, ragged blocks) moves some element
+    by far more than the bf16 rounding of the result."""
+    q_lens = [1, 70, 130, 5]
+    k_lens = [1, 70, 300, 200]
+    hkv = 2
+    dev, host = build_case(gpu_device, hkv, g, bs, q_lens, k_lens, seed=5)
+    nb = host["kc"].shape[0]
+    vc = torch.zeros((nb, bs, hkv, 128), dtype=torch.bfloat16)
+    for i, lk in enumerate(k_lens):
+        for t in range(lk):
+            vc[host["tables"][i, t // bs], t % bs, :, t % 128] = 1.0
+    q0 = torch.zeros_like(dev["q"])
+    out = backend.paged_attention_prefill(q0, dev["kc"], vc.to(gpu_device), dev["tables"],
+                                          dev["cu_q"], dev["cu_k"], 0.7).float().cpu().numpy()
+    for i, (lq, lk) in enumerate(zip(q_lens, k_lens)):
+        for j in range(lq):
+            n = lk - lq + j + 1  # keys 0 .. n-1 visible
+            expect = np.array([len(range(d, n, 128)) for d in range(128)], np.float32) / n
+            got = out[host["cu_q"][i] + j]
+            np.testing.assert_allclose(got, np.broadcast_to(expect, got.shape), rtol=2.0 ** -8,
+                                       atol=0, err_msg=f"request {i} query {j}")
+
+
+def test_unsupported_layouts_raise(backend, gpu_device):
+    dev, _ = build_case(gpu_device, 3, 1, 16, [4], [4], seed=1)
+    q3 = torch.zeros((4, 9, 128), dtype=torch.bfloat16, device=gpu_device)  # G = 3
+    with pytest.raises((ValueError, RuntimeError)):
+        backend.paged_attention_prefill(q3, dev["kc"], dev["vc"], dev["tables"], dev["cu_q"],
+                                        dev["cu_k"], 0.1)
+
+
+def test_chunked_prefill_full_size(backend, gpu_device):
+    """The chunked-prefill step at full size: 16 requests in one 8192-token
+    chunk (lengths uniform in [128, 4096] scaled to the chunk), requests 0-7
+    continuing after 1-4 cached blocks; 8 kv heads x 2 query heads each,
+    256-row blocks.  Every element is checked against the oracle."""
+    rng = np.random.default_rng(17)
+    raw = rng.integers(128, 4097, 16).astype(np.float64)
+    q_lens = np.floor(raw / raw.sum() * 8192).astype(np.int64)
+    q_lens[-1] += 8192 - q_lens.sum()
+    cached = np.zeros(16, np.int64)
+    cached[:8] = rng.integers(1, 5, 8) * 256
+    k_lens = q_lens + cached
+    dev, host = build_case(gpu_device, 8, 2, 256, q_lens.tolist(), k_lens.tolist(), seed=29)
+    scale = 1 / math.sqrt(128)
+    out = run(backend, dev, scale)
+    check_close(out, *reference(host, scale), "chunked prefill")
