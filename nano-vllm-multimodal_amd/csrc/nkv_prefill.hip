@@ -40,37 +40,35 @@ constexpr int kPfRows = kPfWaves * 32;  // query rows per workgroup
 constexpr int kPfKeys = 64;             // keys per tile
 constexpr int kPfDim = 128;             // head_dim
 constexpr int kPfPlanThreads = 1024;
-// LDS row pitches in bf16 elements (padding spreads the 16 rows that one
-// MFMA operand load touches over different banks).
-constexpr int kKPitch = kPfDim + 8;   // K tile [key][d]: 272 B per key
-constexpr int kVPitch = kPfKeys + 8;  // V^T tile [d][key]: 144 B per d
+// V^T tile pitch in bf16 elements: 136 B per dim row, so the 16 rows that
+// one operand load touches start on 16 different bank pairs.
+constexpr int kVPitch = kPfKeys + 4;
+// Lazy softmax reference (log2 units): weights stay <= 2^8 before the final
+// division, far from fp32 / bf16 overflow.
+constexpr float kRescaleLog2 = 8.f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// K tile [key][dim], 256 B per key with the 16-byte chunks of key r stored
+// at chunk ^ (r % 16): an operand load (16 keys at one chunk) then touches
+// 16 different chunk positions.
 struct PrefillShared {
-  uint16_t k[kPfKeys * kKPitch];
+  uint16_t k[kPfKeys * kPfDim];
   uint16_t vt[kPfDim * kVPitch];
-  int32_t valid[kPfKeys];
+  uint8_t valid[kPfKeys];
 };
+
+__device__ __forceinline__ int k_offset(int key, int chunk) {
+  return key * kPfDim + ((chunk ^ (key & 15)) << 3);
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// fp32 -> bf16 bits, round to nearest even (NaN stays a quiet NaN).
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u) return 0x7FC0u;
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
-}
-
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return bf16_bits(lo) | (bf16_bits(hi) << 16);
 }
 
 // Low / high 16-bit halves of two words, packed: {a.lo, b.lo} or {a.hi, b.hi}.
@@ -112,14 +110,106 @@ __global__ __launch_bounds__(kPfPlanThreads) void prefill_plan_kernel(
   }
 }
 
+// Where one sequence's context rows live: its block table and the cache
+// geometry.  Power-of-two block sizes map rows with shifts.
+struct ContextMap {
+  const int32_t* table;
+  int64_t table_stride;
+  int32_t block_size;
+  int32_t block_shift;  // log2(block_size), or -1 when it is not a power of two
+  int32_t num_blocks;
+  int32_t num_keys;     // rows past this are never read
+
+  // Physical cache row of context row t, or -1 when t is past num_keys or
+  // the table, or its block id is outside [0, num_blocks).
+  __device__ __forceinline__ int64_t row(int32_t t) const {
+    int32_t logical, offset;
+    if (block_shift >= 0) {
+      logical = t >> block_shift;
+      offset = t & (block_size - 1);
+    } else {
+      logical = t / block_size;
+      offset = t - logical * block_size;
+    }
+    if (t >= num_keys || logical >= table_stride) return -1;
+    const int32_t block = table[logical];
+    if (block < 0 || block >= num_blocks) return -1;
+    return static_cast<int64_t>(block) * block_size + offset;
+  }
+};
+
+// One thread's share of a key tile in flight: 4 K words (16 B) and the
+// 4 x 8 V block it transposes, plus which of those rows are valid.
+struct TileLoad {
+  u32x4 k[4];
+  u32x4 v[4];
+  uint32_t k_ok;  // bit w: K word w's key is valid
+};
+
+__device__ __forceinline__ TileLoad load_tile(const uint8_t* __restrict__ key_cache,
+                                              const uint8_t* __restrict__ value_cache,
+                                              const ContextMap& map, int64_t row_bytes,
+                                              int64_t head_bytes, int32_t key0, int tid) {
+  TileLoad r;
+  r.k_ok = 0;
+  // K: 64 keys x 16 words of 16 B, 4 words per thread (16 threads per key).
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int idx = w * kPfThreads + tid;
+    const int64_t row = map.row(key0 + (idx >> 4));
+    r.k[w] = u32x4{0u, 0u, 0u, 0u};
+    if (row >= 0) {
+      r.k[w] = reinterpret_cast<const u32x4*>(key_cache + row * row_bytes + head_bytes)[idx & 15];
+      r.k_ok |= 1u << w;
+    }
+  }
+  // V: keys 4 * (tid / 16) .. +4, dims 8 * (tid % 16) .. +8.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t row = map.row(key0 + 4 * (tid >> 4) + j);
+    r.v[j] = u32x4{0u, 0u, 0u, 0u};
+    if (row >= 0) {
+      r.v[j] = reinterpret_cast<const u32x4*>(value_cache + row * row_bytes + head_bytes)[tid & 15];
+    }
+  }
+  return r;
+}
+
+// K rows (swizzled chunks); V transposed: the 4 x 8 block becomes 8 rows
+// (dims) of 4 keys, each stored as 8 bytes.
+__device__ __forceinline__ void stage_tile(PrefillShared& sh, const TileLoad& r, int tid) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int idx = w * kPfThreads + tid;
+    const int key = idx >> 4;
+    const int chunk = idx & 15;
+    *reinterpret_cast<u32x4*>(&sh.k[k_offset(key, chunk)]) = r.k[w];
+    if (chunk == 0) sh.valid[key] = static_cast<uint8_t>((r.k_ok >> w) & 1u);
+  }
+  const int kq = tid >> 4;
+  const int dq = tid & 15;
+  const uint32_t w0[4] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w};
+  const uint32_t w1[4] = {r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w};
+  const uint32_t w2[4] = {r.v[2].x, r.v[2].y, r.v[2].z, r.v[2].w};
+  const uint32_t w3[4] = {r.v[3].x, r.v[3].y, r.v[3].z, r.v[3].w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {  // dims 2c (low halves) and 2c + 1 (high halves)
+    const u32x2 even = {pack_lo(w0[c], w1[c]), pack_lo(w2[c], w3[c])};
+    const u32x2 odd = {pack_hi(w0[c], w1[c]), pack_hi(w2[c], w3[c])};
+    *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c) * kVPitch + 4 * kq]) = even;
+    *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c + 1) * kVPitch + 4 * kq]) = odd;
+  }
+}
+
 template <int G>
 __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_token_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
     const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,
-    int32_t num_blocks, int32_t num_kv_heads, const int32_t* __restrict__ cu_seqlens_q,
-    const int32_t* __restrict__ cu_seqlens_k, const int4* __restrict__ plan, int32_t num_seqs,
-    float scale_log2, uint16_t* __restrict__ out, int64_t out_token_stride) {
+    int32_t block_shift, int32_t num_blocks, int32_t num_kv_heads,
+    const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
+    const int4* __restrict__ plan, int32_t num_seqs, float scale_log2,
+    uint16_t* __restrict__ out, int64_t out_token_stride) {
   constexpr int kTileTokens = kPfRows / G;
   __shared__ PrefillShared sh;
 
@@ -141,7 +231,12 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
   const int c16 = lane & 15;  // the lane's query row inside a 16-row block
   const int g4 = lane >> 4;   // which quarter of the MFMA k dimension the lane holds
   const int64_t row_bytes = static_cast<int64_t>(num_kv_heads) * kPfDim * 2;
-  const int32_t* table = tables + static_cast<int64_t>(seq) * table_stride;
+  const int64_t head_bytes = static_cast<int64_t>(kh) * kPfDim * 2;
+  // keys the last row sees (<= lk); every row sees at least the first one_row_keys
+  const int32_t num_keys = lk - lq + tok0 + ntok;
+  const int32_t first_row_keys = lk - lq + tok0 + 1;
+  const ContextMap map{tables + static_cast<int64_t>(seq) * table_stride, table_stride,
+                       block_size, block_shift, num_blocks, num_keys};
 
   // Q^T operands (B of S^T = K Q^T): lane holds row m, dims 32 * dc + 8 * g4 .. +8.
   bf16x8 qb[2][4];
@@ -162,7 +257,6 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
     }
   }
 
-  const int32_t num_keys = lk - lq + tok0 + ntok;  // keys the last row sees, <= lk
   const int32_t num_tiles = (num_keys + kPfKeys - 1) / kPfKeys;
   float row_max[2] = {-INFINITY, -INFINITY};
   float row_sum[2] = {0.f, 0.f};  // this lane's share of the row's weight sum
@@ -173,59 +267,20 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
     acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Global loads of tile t + 1 are issued before tile t's MFMA work, so
+  // their latency overlaps it; they land in LDS after the next barrier.
+  TileLoad pending = load_tile(key_cache, value_cache, map, row_bytes, head_bytes, 0, tid);
   for (int32_t tile = 0; tile < num_tiles; ++tile) {
     const int32_t key0 = tile * kPfKeys;
     __syncthreads();  // the previous tile's LDS reads are done
-    // K tile: 64 keys x 16 words of 16 B, 4 words per thread, row-major.
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int idx = w * kPfThreads + tid;
-      const int key = idx >> 4;
-      const int dch = idx & 15;
-      const int32_t t = key0 + key;
-      const int32_t logical = t / block_size;
-      int32_t block = -1;
-      if (t < num_keys && logical < table_stride) block = table[logical];
-      const bool ok = block >= 0 && block < num_blocks;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (ok) {
-        const int64_t row = static_cast<int64_t>(block) * block_size + t % block_size;
-        v = reinterpret_cast<const u32x4*>(key_cache + row * row_bytes + kh * kPfDim * 2)[dch];
-      }
-      *reinterpret_cast<u32x4*>(&sh.k[key * kKPitch + dch * 8]) = v;
-      if (dch == 0) sh.valid[key] = ok ? 1 : 0;
+    stage_tile(sh, pending, tid);
+    // A tile is plain when every row sees all its keys and all are valid:
+    // its scores need no mask.
+    const bool plain = __syncthreads_and(pending.k_ok == 0xFu) != 0 &&
+                       key0 + kPfKeys <= first_row_keys;
+    if (tile + 1 < num_tiles) {
+      pending = load_tile(key_cache, value_cache, map, row_bytes, head_bytes, key0 + kPfKeys, tid);
     }
-    // V tile transposed: thread -> 4 keys x 8 dims, stored as 8 rows of 4 keys.
-    {
-      const int kq = tid >> 4;  // keys 4 * kq .. +4
-      const int dq = tid & 15;  // dims 8 * dq .. +8
-      u32x4 r[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int32_t t = key0 + 4 * kq + j;
-        const int32_t logical = t / block_size;
-        int32_t block = -1;
-        if (t < num_keys && logical < table_stride) block = table[logical];
-        r[j] = u32x4{0u, 0u, 0u, 0u};
-        if (block >= 0 && block < num_blocks) {
-          const int64_t row = static_cast<int64_t>(block) * block_size + t % block_size;
-          r[j] = reinterpret_cast<const u32x4*>(value_cache + row * row_bytes +
-                                                 kh * kPfDim * 2)[dq];
-        }
-      }
-      const uint32_t w0[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
-      const uint32_t w1[4] = {r[1].x, r[1].y, r[1].z, r[1].w};
-      const uint32_t w2[4] = {r[2].x, r[2].y, r[2].z, r[2].w};
-      const uint32_t w3[4] = {r[3].x, r[3].y, r[3].z, r[3].w};
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {  // dims 2c (low halves) and 2c + 1 (high halves)
-        const u32x2 even = {pack_lo(w0[c], w1[c]), pack_lo(w2[c], w3[c])};
-        const u32x2 odd = {pack_hi(w0[c], w1[c]), pack_hi(w2[c], w3[c])};
-        *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c) * kVPitch + 4 * kq]) = even;
-        *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c + 1) * kVPitch + 4 * kq]) = odd;
-      }
-    }
-    __syncthreads();
 
     // S^T = K Q^T: block (kb, mb) holds keys 16 kb + 4 g4 + i of row m.
     f32x4 st[4][2];
@@ -236,7 +291,7 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) {
         const bf16x8 a = as_bf16x8(
-            *reinterpret_cast<const u32x4*>(&sh.k[(16 * kb + c16) * kKPitch + 32 * dc + 8 * g4]));
+            *reinterpret_cast<const u32x4*>(&sh.k[k_offset(16 * kb + c16, 4 * dc + g4)]));
         st[kb][0] = mfma(a, qb[0][dc], st[kb][0]);
         st[kb][1] = mfma(a, qb[1][dc], st[kb][1]);
       }
@@ -246,49 +301,55 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
     bf16x8 pb[2][2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      float s[4][4];
-      float local = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = 16 * kb + 4 * g4 + i;
-          const bool visible = key0 + key <= limit[mb] && sh.valid[key] != 0;
-          s[kb][i] = visible ? st[kb][mb][i] * scale_log2 : -INFINITY;
-          local = fmaxf(local, s[kb][i]);
-        }
-      }
-      local = fmaxf(local, __shfl_xor(local, 16, kWave));
-      local = fmaxf(local, __shfl_xor(local, 32, kWave));
-      const float m_new = fmaxf(row_max[mb], local);
-      float p[4][4];
-      float psum = 0.f;
-      if (m_new == -INFINITY) {  // nothing visible yet in this row
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) p[kb][i] = 0.f;
-      } else {
-        const float alpha = __builtin_amdgcn_exp2f(row_max[mb] - m_new);  // 0 when row_max is -inf
-        row_sum[mb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) acc[db][mb] *= alpha;
+      if (!plain) {  // hide keys past the row's limit or in invalid blocks
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            p[kb][i] = __builtin_amdgcn_exp2f(s[kb][i] - m_new);  // exp2(-inf) = 0 for hidden keys
-            psum += p[kb][i];
+            const int key = 16 * kb + 4 * g4 + i;
+            if (key0 + key > limit[mb] || sh.valid[key] == 0) st[kb][mb][i] = -INFINITY;
           }
+      }
+      float local = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) local = fmaxf(local, st[kb][mb][i]);
+      local = fmaxf(local, __shfl_xor(local, 16, kWave));
+      local = fmaxf(local, __shfl_xor(local, 32, kWave));
+      local *= scale_log2;  // scale > 0, so the max commutes with it
+      // The row's reference max moves only when a score passes it by more
+      // than kRescaleLog2 (always for the first visible score), so the
+      // rescale of the accumulators is rare after the first tiles.
+      const bool move = local > row_max[mb] + kRescaleLog2;
+      if (__any(move)) {
+        const float m_new = move ? local : row_max[mb];
+        const float alpha = move ? __builtin_amdgcn_exp2f(row_max[mb] - m_new) : 1.f;
+        row_sum[mb] *= alpha;  // alpha = 0 when the old reference was -inf
+#pragma unroll
+        for (int db = 0; db < 8; ++db) acc[db][mb] *= alpha;
         row_max[mb] = m_new;
       }
-      row_sum[mb] += psum;
+      // A row with nothing visible yet keeps the reference -inf: its
+      // weights are 0 (hidden scores are -inf too).
+      const float ref = row_max[mb] == -INFINITY ? INFINITY : row_max[mb];
+      float p[4][4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][mb][i], scale_log2, -ref));
+          row_sum[mb] += p[kb][i];
+        }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const u32x4 w = {pack_bf16(p[2 * c][0], p[2 * c][1]), pack_bf16(p[2 * c][2], p[2 * c][3]),
-                         pack_bf16(p[2 * c + 1][0], p[2 * c + 1][1]),
-                         pack_bf16(p[2 * c + 1][2], p[2 * c + 1][3])};
-        pb[c][mb] = as_bf16x8(w);
+        bf16x8 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w[i] = static_cast<__bf16>(p[2 * c][i]);
+          w[4 + i] = static_cast<__bf16>(p[2 * c + 1][i]);
+        }
+        pb[c][mb] = w;
       }
     }
 
@@ -324,14 +385,15 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const f32x4 v = acc[db][mb];
-      const u32x2 w = {pack_bf16(v.x * inv, v.y * inv), pack_bf16(v.z * inv, v.w * inv)};
-      *reinterpret_cast<u32x2*>(orow + 16 * db + 4 * g4) = w;
+      const bf16x4 w = {static_cast<__bf16>(v.x * inv), static_cast<__bf16>(v.y * inv),
+                        static_cast<__bf16>(v.z * inv), static_cast<__bf16>(v.w * inv)};
+      *reinterpret_cast<bf16x4*>(orow + 16 * db + 4 * g4) = w;
     }
   }
 }
 
 using PrefillKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const uint8_t*,
-                               const int32_t*, int64_t, int32_t, int32_t, int32_t,
+                               const int32_t*, int64_t, int32_t, int32_t, int32_t, int32_t,
                                const int32_t*, const int32_t*, const int4*, int32_t, float,
                                uint16_t*, int64_t);
 
@@ -437,11 +499,19 @@ extern "C" int nkv_paged_attention_prefill(
                     "rows 8-byte aligned");
   }
   const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
+  if (!(scale_log2 > 0.f)) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: scale must be positive");
+  }
+  int32_t block_shift = -1;
+  if ((block_size & (block_size - 1)) == 0) {
+    block_shift = 0;
+    while ((int64_t{1} << block_shift) < block_size) ++block_shift;
+  }
   kernel<<<dim3(static_cast<unsigned>(capacity), static_cast<unsigned>(num_kv_heads)),
            dim3(kPfThreads), 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(q), q_token_stride, static_cast<const uint8_t*>(key_cache),
       static_cast<const uint8_t*>(value_cache), block_tables, table_stride,
-      static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
+      static_cast<int32_t>(block_size), block_shift, static_cast<int32_t>(num_blocks),
       static_cast<int32_t>(num_kv_heads), cu_seqlens_q, cu_seqlens_k,
       static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2,
       static_cast<uint16_t*>(out), out_token_stride);
