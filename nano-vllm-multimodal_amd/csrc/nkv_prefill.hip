@@ -40,9 +40,7 @@ constexpr int kPfRows = kPfWaves * 32;  // query rows per workgroup
 constexpr int kPfKeys = 64;             // keys per tile
 constexpr int kPfDim = 128;             // head_dim
 constexpr int kPfPlanThreads = 1024;
-// V^T tile pitch in bf16 elements: 136 B per dim row, so the 16 rows that
-// one operand load touches start on 16 different bank pairs.
-constexpr int kVPitch = kPfKeys + 4;
+
 // Lazy softmax reference (log2 units): weights stay <= 2^8 before the final
 // division, far from fp32 / bf16 overflow.
 constexpr float kRescaleLog2 = 8.f;
@@ -54,15 +52,37 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // K tile [key][dim], 256 B per key with the 16-byte chunks of key r stored
 // at chunk ^ (r % 16): an operand load (16 keys at one chunk) then touches
-// 16 different chunk positions.
+// 16 different chunk positions.  V^T tile [dim][key], 128 B per dim with the
+// 8-byte units (4 keys) of dim d stored at unit ^ ((d ^ d / 8) % 16): the
+// operand loads (16 consecutive dims at one unit) hit 16 different units,
+// and the staging stores (dims 8 apart) at least 8.
+// The arrays are typed by access width so that every LDS access is one
+// 16- or 8-byte instruction.
 struct PrefillShared {
-  uint16_t k[kPfKeys * kPfDim];
-  uint16_t vt[kPfDim * kVPitch];
-  uint8_t valid[kPfKeys];
+  u32x4 k[kPfKeys * 16];                  // [key][16-byte chunk]
+  u32x2 vt[kPfDim * 16];                  // [dim][8-byte unit of 4 keys]
+  int4 rows[2][kPfKeys / 4];              // physical row of each key of a tile, -1 if invalid
 };
 
-__device__ __forceinline__ int k_offset(int key, int chunk) {
-  return key * kPfDim + ((chunk ^ (key & 15)) << 3);
+__device__ __forceinline__ int k_index(int key, int chunk) { return key * 16 + (chunk ^ (key & 15)); }
+
+__device__ __forceinline__ int vt_index(int dim, int unit) {
+  return dim * 16 + (unit ^ ((dim ^ (dim >> 3)) & 15));
+}
+
+// Max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row's
+// lanes), with the cross-row swaps of gfx950 (no LDS traffic).
+__device__ __forceinline__ float row4_max(float x) {
+  auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float row4_sum(float x) {
+  auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -122,7 +142,7 @@ struct ContextMap {
 
   // Physical cache row of context row t, or -1 when t is past num_keys or
   // the table, or its block id is outside [0, num_blocks).
-  __device__ __forceinline__ int64_t row(int32_t t) const {
+  __device__ __forceinline__ int32_t row(int32_t t) const {
     int32_t logical, offset;
     if (block_shift >= 0) {
       logical = t >> block_shift;
@@ -134,7 +154,7 @@ struct ContextMap {
     if (t >= num_keys || logical >= table_stride) return -1;
     const int32_t block = table[logical];
     if (block < 0 || block >= num_blocks) return -1;
-    return static_cast<int64_t>(block) * block_size + offset;
+    return block * block_size + offset;  // num_blocks * block_size <= INT32_MAX
   }
 };
 
@@ -146,17 +166,19 @@ struct TileLoad {
   uint32_t k_ok;  // bit w: K word w's key is valid
 };
 
+// The loads of one tile, from the physical rows its keys map to (resolved
+// once per tile by 64 threads into LDS).
 __device__ __forceinline__ TileLoad load_tile(const uint8_t* __restrict__ key_cache,
                                               const uint8_t* __restrict__ value_cache,
-                                              const ContextMap& map, int64_t row_bytes,
-                                              int64_t head_bytes, int32_t key0, int tid) {
+                                              const int32_t* __restrict__ rows, int64_t row_bytes,
+                                              int64_t head_bytes, int tid) {
   TileLoad r;
   r.k_ok = 0;
   // K: 64 keys x 16 words of 16 B, 4 words per thread (16 threads per key).
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const int idx = w * kPfThreads + tid;
-    const int64_t row = map.row(key0 + (idx >> 4));
+    const int32_t row = rows[idx >> 4];
     r.k[w] = u32x4{0u, 0u, 0u, 0u};
     if (row >= 0) {
       r.k[w] = reinterpret_cast<const u32x4*>(key_cache + row * row_bytes + head_bytes)[idx & 15];
@@ -166,7 +188,7 @@ __device__ __forceinline__ TileLoad load_tile(const uint8_t* __restrict__ key_ca
   // V: keys 4 * (tid / 16) .. +4, dims 8 * (tid % 16) .. +8.
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t row = map.row(key0 + 4 * (tid >> 4) + j);
+    const int32_t row = rows[4 * (tid >> 4) + j];
     r.v[j] = u32x4{0u, 0u, 0u, 0u};
     if (row >= 0) {
       r.v[j] = reinterpret_cast<const u32x4*>(value_cache + row * row_bytes + head_bytes)[tid & 15];
@@ -183,8 +205,7 @@ __device__ __forceinline__ void stage_tile(PrefillShared& sh, const TileLoad& r,
     const int idx = w * kPfThreads + tid;
     const int key = idx >> 4;
     const int chunk = idx & 15;
-    *reinterpret_cast<u32x4*>(&sh.k[k_offset(key, chunk)]) = r.k[w];
-    if (chunk == 0) sh.valid[key] = static_cast<uint8_t>((r.k_ok >> w) & 1u);
+    sh.k[k_index(key, chunk)] = r.k[w];
   }
   const int kq = tid >> 4;
   const int dq = tid & 15;
@@ -196,8 +217,8 @@ __device__ __forceinline__ void stage_tile(PrefillShared& sh, const TileLoad& r,
   for (int c = 0; c < 4; ++c) {  // dims 2c (low halves) and 2c + 1 (high halves)
     const u32x2 even = {pack_lo(w0[c], w1[c]), pack_lo(w2[c], w3[c])};
     const u32x2 odd = {pack_hi(w0[c], w1[c]), pack_hi(w2[c], w3[c])};
-    *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c) * kVPitch + 4 * kq]) = even;
-    *reinterpret_cast<u32x2*>(&sh.vt[(8 * dq + 2 * c + 1) * kVPitch + 4 * kq]) = odd;
+    sh.vt[vt_index(8 * dq + 2 * c, kq)] = even;
+    sh.vt[vt_index(8 * dq + 2 * c + 1, kq)] = odd;
   }
 }
 
@@ -269,17 +290,26 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
 
   // Global loads of tile t + 1 are issued before tile t's MFMA work, so
   // their latency overlaps it; they land in LDS after the next barrier.
-  TileLoad pending = load_tile(key_cache, value_cache, map, row_bytes, head_bytes, 0, tid);
+  // Each tile's 64 key rows are resolved through the block table by 64
+  // threads into LDS one tile ahead.
+  int32_t* const rows0 = reinterpret_cast<int32_t*>(sh.rows[0]);
+  int32_t* const rows1 = reinterpret_cast<int32_t*>(sh.rows[1]);
+  if (tid < kPfKeys) rows0[tid] = map.row(tid);
+  __syncthreads();
+  TileLoad pending = load_tile(key_cache, value_cache, rows0, row_bytes, head_bytes, tid);
   for (int32_t tile = 0; tile < num_tiles; ++tile) {
     const int32_t key0 = tile * kPfKeys;
+    int32_t* const rows_next = (tile & 1) ? rows0 : rows1;
+    const int4* const rows_now = sh.rows[tile & 1];
     __syncthreads();  // the previous tile's LDS reads are done
     stage_tile(sh, pending, tid);
+    if (tid < kPfKeys && tile + 1 < num_tiles) rows_next[tid] = map.row(key0 + kPfKeys + tid);
     // A tile is plain when every row sees all its keys and all are valid:
     // its scores need no mask.
     const bool plain = __syncthreads_and(pending.k_ok == 0xFu) != 0 &&
                        key0 + kPfKeys <= first_row_keys;
     if (tile + 1 < num_tiles) {
-      pending = load_tile(key_cache, value_cache, map, row_bytes, head_bytes, key0 + kPfKeys, tid);
+      pending = load_tile(key_cache, value_cache, rows_next, row_bytes, head_bytes, tid);
     }
 
     // S^T = K Q^T: block (kb, mb) holds keys 16 kb + 4 g4 + i of row m.
@@ -290,8 +320,7 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
       st[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) {
-        const bf16x8 a = as_bf16x8(
-            *reinterpret_cast<const u32x4*>(&sh.k[k_offset(16 * kb + c16, 4 * dc + g4)]));
+        const bf16x8 a = as_bf16x8(sh.k[k_index(16 * kb + c16, 4 * dc + g4)]);
         st[kb][0] = mfma(a, qb[0][dc], st[kb][0]);
         st[kb][1] = mfma(a, qb[1][dc], st[kb][1]);
       }
@@ -303,21 +332,21 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
     for (int mb = 0; mb < 2; ++mb) {
       if (!plain) {  // hide keys past the row's limit or in invalid blocks
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int kb = 0; kb < 4; ++kb) {
+          const int4 r = rows_now[4 * kb + g4];  // rows of keys 16 kb + 4 g4 + i
+          const int32_t row[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int key = 16 * kb + 4 * g4 + i;
-            if (key0 + key > limit[mb] || sh.valid[key] == 0) st[kb][mb][i] = -INFINITY;
+            if (key0 + 16 * kb + 4 * g4 + i > limit[mb] || row[i] < 0) st[kb][mb][i] = -INFINITY;
           }
+        }
       }
       float local = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) local = fmaxf(local, st[kb][mb][i]);
-      local = fmaxf(local, __shfl_xor(local, 16, kWave));
-      local = fmaxf(local, __shfl_xor(local, 32, kWave));
-      local *= scale_log2;  // scale > 0, so the max commutes with it
+      local = row4_max(local) * scale_log2;  // scale > 0, so the max commutes with it
       // The row's reference max moves only when a score passes it by more
       // than kRescaleLog2 (always for the first visible score), so the
       // rescale of the accumulators is rare after the first tiles.
@@ -358,11 +387,11 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
     // 32c + 16 + 4 g4 + j.
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
-      const uint16_t* vrow = &sh.vt[(16 * db + c16) * kVPitch];
+      const int dim = 16 * db + c16;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 32 * c + 4 * g4);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 32 * c + 16 + 4 * g4);
+        const u32x2 lo = sh.vt[vt_index(dim, 8 * c + g4)];
+        const u32x2 hi = sh.vt[vt_index(dim, 8 * c + 4 + g4)];
         const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
         acc[db][0] = mfma(a, pb[c][0], acc[db][0]);
         acc[db][1] = mfma(a, pb[c][1], acc[db][1]);
@@ -373,9 +402,7 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
   // Normalise and store: the row's weight sum is spread over its 4 lanes.
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
-    float total = row_sum[mb];
-    total += __shfl_xor(total, 16, kWave);
-    total += __shfl_xor(total, 32, kWave);
+    const float total = row4_sum(row_sum[mb]);
     const int m = wave * 32 + mb * 16 + c16;
     const int t = m / G;
     if (t >= ntok) continue;
