@@ -56,18 +56,30 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // 8-byte units (4 keys) of dim d stored at unit ^ ((d ^ d / 8) % 16): the
 // operand loads (16 consecutive dims at one unit) hit 16 different units,
 // and the staging stores (dims 8 apart) at least 8.
-// The arrays are typed by access width so that every LDS access is one
-// 16- or 8-byte instruction.
+// K and V tiles, double-buffered, copied straight from global memory into
+// LDS by global_load_lds (one wavefront instruction fills 1 KiB of
+// consecutive LDS: 4 keys x 256 B; the source address of each lane picks
+// the chunk that belongs at its position).  Both are [key][16-byte chunk],
+// the chunks of key r swizzled so that the MFMA operand reads are
+// conflict-free:
+//   K: chunk c at c ^ (r % 16)    (ds_read_b128: 16 keys at one chunk)
+//   V: chunk c at c ^ 2 (r % 8)   (ds_read_b64_tr_b16: 16 keys x 32 bytes)
 struct PrefillShared {
-  u32x4 k[kPfKeys * 16];                  // [key][16-byte chunk]
-  u32x2 vt[kPfDim * 16];                  // [dim][8-byte unit of 4 keys]
-  int4 rows[2][kPfKeys / 4];              // physical row of each key of a tile, -1 if invalid
+  u32x4 k[2][kPfKeys * 16];
+  u32x4 v[2][kPfKeys * 16];
+  int32_t rows[3][kPfKeys];  // physical row of each key of a tile, -1 if invalid
+  int32_t invalid[3];        // whether a tile has an invalid row
 };
 
 __device__ __forceinline__ int k_index(int key, int chunk) { return key * 16 + (chunk ^ (key & 15)); }
+__device__ __forceinline__ int v_index(int key, int chunk) {
+  return key * 16 + (chunk ^ ((key & 7) << 1));
+}
 
-__device__ __forceinline__ int vt_index(int dim, int unit) {
-  return dim * 16 + (unit ^ ((dim ^ (dim >> 3)) & 15));
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // Max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row's
@@ -83,20 +95,6 @@ __device__ __forceinline__ float row4_sum(float x) {
   x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
   p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// Low / high 16-bit halves of two words, packed: {a.lo, b.lo} or {a.hi, b.hi}.
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
 // Plan: one int4 {seq, token0, tokens, 0} per workgroup: tokens [token0,
@@ -158,68 +156,48 @@ struct ContextMap {
   }
 };
 
-// One thread's share of a key tile in flight: 4 K words (16 B) and the
-// 4 x 8 V block it transposes, plus which of those rows are valid.
-struct TileLoad {
-  u32x4 k[4];
-  u32x4 v[4];
-  uint32_t k_ok;  // bit w: K word w's key is valid
-};
-
-// The loads of one tile, from the physical rows its keys map to (resolved
-// once per tile by 64 threads into LDS).
-__device__ __forceinline__ TileLoad load_tile(const uint8_t* __restrict__ key_cache,
-                                              const uint8_t* __restrict__ value_cache,
-                                              const int32_t* __restrict__ rows, int64_t row_bytes,
-                                              int64_t head_bytes, int tid) {
-  TileLoad r;
-  r.k_ok = 0;
-  // K: 64 keys x 16 words of 16 B, 4 words per thread (16 threads per key).
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const int idx = w * kPfThreads + tid;
-    const int32_t row = rows[idx >> 4];
-    r.k[w] = u32x4{0u, 0u, 0u, 0u};
-    if (row >= 0) {
-      r.k[w] = reinterpret_cast<const u32x4*>(key_cache + row * row_bytes + head_bytes)[idx & 15];
-      r.k_ok |= 1u << w;
-    }
-  }
-  // V: keys 4 * (tid / 16) .. +4, dims 8 * (tid % 16) .. +8.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int32_t row = rows[4 * (tid >> 4) + j];
-    r.v[j] = u32x4{0u, 0u, 0u, 0u};
-    if (row >= 0) {
-      r.v[j] = reinterpret_cast<const u32x4*>(value_cache + row * row_bytes + head_bytes)[tid & 15];
-    }
-  }
-  return r;
+// Wavefront 0 resolves the 64 rows of the tile starting at key0 (one per
+// lane) and whether any of them is invalid.
+__device__ __forceinline__ void resolve_rows(PrefillShared& sh, int slot, const ContextMap& map,
+                                             int32_t key0, int lane) {
+  const int32_t row = map.row(key0 + lane);
+  sh.rows[slot][lane] = row;
+  const bool any_invalid = __any(row < 0);
+  if (lane == 0) sh.invalid[slot] = any_invalid ? 1 : 0;
 }
 
-// K rows (swizzled chunks); V transposed: the 4 x 8 block becomes 8 rows
-// (dims) of 4 keys, each stored as 8 bytes.
-__device__ __forceinline__ void stage_tile(PrefillShared& sh, const TileLoad& r, int tid) {
+// This wavefront's share of one tile's copies: keys 16 w .. 16 w + 15, K
+// and V, 4 keys per instruction.  An invalid row reads the start of the
+// cache instead (in bounds); its K scores are masked and its V zeroed.
+__device__ __forceinline__ void issue_tile(PrefillShared& sh, int buf, const int32_t* rows,
+                                           const uint8_t* key_cache, const uint8_t* value_cache,
+                                           int64_t row_bytes, int64_t head_bytes, int wave,
+                                           int lane) {
+  const int pos = lane & 15;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const int idx = w * kPfThreads + tid;
-    const int key = idx >> 4;
-    const int chunk = idx & 15;
-    sh.k[k_index(key, chunk)] = r.k[w];
+  for (int i = 0; i < 4; ++i) {
+    const int key0 = 16 * wave + 4 * i;
+    const int key = key0 + (lane >> 4);
+    const int32_t row = rows[key];
+    const int64_t base = row >= 0 ? row * row_bytes + head_bytes : 0;
+    __builtin_amdgcn_global_load_lds(key_cache + base + 16 * (pos ^ (key & 15)),
+                                     &sh.k[buf][key0 * 16], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(value_cache + base + 16 * (pos ^ ((key & 7) << 1)),
+                                     &sh.v[buf][key0 * 16], 16, 0, 0);
   }
-  const int kq = tid >> 4;
-  const int dq = tid & 15;
-  const uint32_t w0[4] = {r.v[0].x, r.v[0].y, r.v[0].z, r.v[0].w};
-  const uint32_t w1[4] = {r.v[1].x, r.v[1].y, r.v[1].z, r.v[1].w};
-  const uint32_t w2[4] = {r.v[2].x, r.v[2].y, r.v[2].z, r.v[2].w};
-  const uint32_t w3[4] = {r.v[3].x, r.v[3].y, r.v[3].z, r.v[3].w};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {  // dims 2c (low halves) and 2c + 1 (high halves)
-    const u32x2 even = {pack_lo(w0[c], w1[c]), pack_lo(w2[c], w3[c])};
-    const u32x2 odd = {pack_hi(w0[c], w1[c]), pack_hi(w2[c], w3[c])};
-    sh.vt[vt_index(8 * dq + 2 * c, kq)] = even;
-    sh.vt[vt_index(8 * dq + 2 * c + 1, kq)] = odd;
-  }
+}
+
+// Four consecutive bf16 of V^T for the PV product: lane 16 G + 4 j + q
+// supplies the address of V[key][dim4 .. +4] and receives, as lane 16 G + i,
+// V[key of lane 16 G + 4 j'][dim of lane 16 G + i] for j' = 0..3 (the
+// gfx950 transposing LDS read).
+__device__ __forceinline__ u32x2 v_tr_read(const PrefillShared& sh, int buf, int key, int dim4) {
+  const int byte = (v_index(key, dim4 >> 3) << 4) + ((dim4 & 7) << 1);
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) char lds_char;
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  lds_v4i16* p = (lds_v4i16*)((lds_char*)(&sh.v[buf][0]) + byte);  // generic -> LDS
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
 
 template <int G>
@@ -253,7 +231,7 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
   const int g4 = lane >> 4;   // which quarter of the MFMA k dimension the lane holds
   const int64_t row_bytes = static_cast<int64_t>(num_kv_heads) * kPfDim * 2;
   const int64_t head_bytes = static_cast<int64_t>(kh) * kPfDim * 2;
-  // keys the last row sees (<= lk); every row sees at least the first one_row_keys
+  // keys the last row sees (<= lk); every row sees at least first_row_keys
   const int32_t num_keys = lk - lq + tok0 + ntok;
   const int32_t first_row_keys = lk - lq + tok0 + 1;
   const ContextMap map{tables + static_cast<int64_t>(seq) * table_stride, table_stride,
@@ -288,29 +266,39 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
     acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Global loads of tile t + 1 are issued before tile t's MFMA work, so
-  // their latency overlaps it; they land in LDS after the next barrier.
-  // Each tile's 64 key rows are resolved through the block table by 64
-  // threads into LDS one tile ahead.
-  int32_t* const rows0 = reinterpret_cast<int32_t*>(sh.rows[0]);
-  int32_t* const rows1 = reinterpret_cast<int32_t*>(sh.rows[1]);
-  if (tid < kPfKeys) rows0[tid] = map.row(tid);
+  // Rows are resolved two tiles ahead (slots rotate over 3); the copies of
+  // tile t + 1 are in flight while tile t is computed.
+  if (wave == 0) {
+    resolve_rows(sh, 0, map, 0, lane);
+    if (num_tiles > 1) resolve_rows(sh, 1, map, kPfKeys, lane);
+  }
   __syncthreads();
-  TileLoad pending = load_tile(key_cache, value_cache, rows0, row_bytes, head_bytes, tid);
+  issue_tile(sh, 0, sh.rows[0], key_cache, value_cache, row_bytes, head_bytes, wave, lane);
+  int slot = 0;  // rows slot of the current tile
   for (int32_t tile = 0; tile < num_tiles; ++tile) {
     const int32_t key0 = tile * kPfKeys;
-    int32_t* const rows_next = (tile & 1) ? rows0 : rows1;
-    const int4* const rows_now = sh.rows[tile & 1];
-    __syncthreads();  // the previous tile's LDS reads are done
-    stage_tile(sh, pending, tid);
-    if (tid < kPfKeys && tile + 1 < num_tiles) rows_next[tid] = map.row(key0 + kPfKeys + tid);
+    const int cur = tile & 1;
+    const int slot1 = slot == 2 ? 0 : slot + 1;
+    const int slot2 = slot1 == 2 ? 0 : slot1 + 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of the tile have landed
+    __syncthreads();                // ... and everyone's; the previous tile is consumed
+    const bool has_invalid = sh.invalid[slot] != 0;
+    if (has_invalid) {  // zero V of invalid rows (what the cache start held may be anything)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int idx = i * kPfThreads + tid;
+        if (sh.rows[slot][idx >> 4] < 0) sh.v[cur][idx] = u32x4{0u, 0u, 0u, 0u};
+      }
+      __syncthreads();
+    }
+    if (tile + 1 < num_tiles) {
+      issue_tile(sh, cur ^ 1, sh.rows[slot1], key_cache, value_cache, row_bytes, head_bytes,
+                 wave, lane);
+    }
+    if (wave == 0 && tile + 2 < num_tiles) resolve_rows(sh, slot2, map, key0 + 2 * kPfKeys, lane);
     // A tile is plain when every row sees all its keys and all are valid:
     // its scores need no mask.
-    const bool plain = __syncthreads_and(pending.k_ok == 0xFu) != 0 &&
-                       key0 + kPfKeys <= first_row_keys;
-    if (tile + 1 < num_tiles) {
-      pending = load_tile(key_cache, value_cache, rows_next, row_bytes, head_bytes, tid);
-    }
+    const bool plain = !has_invalid && key0 + kPfKeys <= first_row_keys;
 
     // S^T = K Q^T: block (kb, mb) holds keys 16 kb + 4 g4 + i of row m.
     f32x4 st[4][2];
@@ -320,7 +308,7 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
       st[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) {
-        const bf16x8 a = as_bf16x8(sh.k[k_index(16 * kb + c16, 4 * dc + g4)]);
+        const bf16x8 a = as_bf16x8(sh.k[cur][k_index(16 * kb + c16, 4 * dc + g4)]);
         st[kb][0] = mfma(a, qb[0][dc], st[kb][0]);
         st[kb][1] = mfma(a, qb[1][dc], st[kb][1]);
       }
@@ -328,9 +316,10 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
 
     // Online softmax per row (exp2 units); P^T operands for both 32-key steps.
     bf16x8 pb[2][2];
+    const int4* rows_now = reinterpret_cast<const int4*>(sh.rows[slot]);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
-      if (!plain) {  // hide keys past the row's limit or in invalid blocks
+      if (!plain) {  // hide keys past the row's limit or in invalid rows
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
           const int4 r = rows_now[4 * kb + g4];  // rows of keys 16 kb + 4 g4 + i
@@ -384,19 +373,21 @@ __global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
 
     // O^T += V^T P^T.  Step c covers keys 32 c .. +32 in the order the P^T
     // operand holds them: slots 0-3 = keys 32c + 4 g4 + j, slots 4-7 = keys
-    // 32c + 16 + 4 g4 + j.
+    // 32c + 16 + 4 g4 + j; the transposing reads deliver V^T in that order.
+    const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses, within 16
+    const int tr_dim = 4 * (lane & 3);              // first dim this lane addresses, within 16
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
-      const int dim = 16 * db + c16;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const u32x2 lo = sh.vt[vt_index(dim, 8 * c + g4)];
-        const u32x2 hi = sh.vt[vt_index(dim, 8 * c + 4 + g4)];
+        const u32x2 lo = v_tr_read(sh, cur, 32 * c + tr_key, 16 * db + tr_dim);
+        const u32x2 hi = v_tr_read(sh, cur, 32 * c + 16 + tr_key, 16 * db + tr_dim);
         const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
         acc[db][0] = mfma(a, pb[c][0], acc[db][0]);
         acc[db][1] = mfma(a, pb[c][1], acc[db][1]);
       }
     }
+    slot = slot1;
   }
 
   // Normalise and store: the row's weight sum is spread over its 4 lanes.
