@@ -201,7 +201,7 @@ __device__ __forceinline__ u32x2 v_tr_read(const PrefillShared& sh, int buf, int
 }
 
 template <int G>
-__global__ __launch_bounds__(kPfThreads) void attn_prefill_kernel(
+__global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_token_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
     const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,
