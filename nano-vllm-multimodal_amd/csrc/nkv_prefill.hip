@@ -98,8 +98,10 @@ __device__ __forceinline__ float row4_sum(float x) {
 }
 
 // Plan: one int4 {seq, token0, tokens, 0} per workgroup: tokens [token0,
-// token0 + tokens) of sequence seq's queries, tokens <= tile_tokens.
-// Entries past the total get tokens = 0.
+// token0 + tokens) of sequence seq's queries, tokens <= tile_tokens.  A
+// sequence's tiles are listed last tile first: later queries see more keys,
+// so the longest workgroups are dispatched first and the short ones fill
+// the tail.  Entries past the total get tokens = 0.
 __global__ __launch_bounds__(kPfPlanThreads) void prefill_plan_kernel(
     const int32_t* __restrict__ cu_seqlens_q, int32_t num_seqs, int32_t tile_tokens,
     int4* __restrict__ plan, int64_t capacity) {
@@ -120,7 +122,8 @@ __global__ __launch_bounds__(kPfPlanThreads) void prefill_plan_kernel(
     int4 entry = make_int4(0, 0, 0, 0);
     if (e < total) {
       const int32_t i = owner_of(s_first, num_seqs, static_cast<int32_t>(e));
-      const int32_t t0 = (static_cast<int32_t>(e) - s_first[i]) * tile_tokens;
+      const int32_t tiles = s_first[i + 1] - s_first[i];
+      const int32_t t0 = (tiles - 1 - (static_cast<int32_t>(e) - s_first[i])) * tile_tokens;
       const int32_t len = cu_seqlens_q[i + 1] - cu_seqlens_q[i];
       entry = make_int4(i, t0, min(tile_tokens, len - t0), 0);
     }

@@ -109,7 +109,7 @@ def test_plan_tiles_cover_every_query(backend, gpu_device):
     entries = plan[: sum(expect)]
     for i, n in enumerate(q_lens):
         own = entries[entries[:, 0] == i]
-        assert own[:, 1].tolist() == list(range(0, n, tile))
+        assert own[:, 1].tolist() == list(range(0, n, tile))[::-1]  # last tile first
         assert int(own[:, 2].sum()) == n
     assert not plan[sum(expect):, 2].any()
 
