@@ -1,0 +1,95 @@
+"""Drop-ins for the two flash-attn calls of the reference's Attention.forward
+(nanovllm/layers/attention.py:5 imports them; :105-116 prefill, :122-130
+decode), run by the hip paged-attention kernels on the paged KV cache.  A
+ROCm build of the engine replaces ``from flash_attn import
+flash_attn_varlen_func, flash_attn_with_kvcache`` with an import from this
+module; the calls stay as they are.
+
+Only what the reference passes is supported: causal attention, bfloat16,
+head_dim 128, 1/2/4/8 query heads per kv head, no dropout, window, alibi or
+softcap.  Anything else raises instead of computing something different.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from nanokv.paged_kv.base import index_value_validation_enabled
+from nanokv.paged_kv.hip_backend import HIPPagedKVBackend
+
+_BACKEND = HIPPagedKVBackend()
+_UNSUPPORTED_DEFAULTS = {
+    "dropout_p": 0.0,
+    "window_size": (-1, -1),
+    "softcap": 0.0,
+    "alibi_slopes": None,
+    "deterministic": False,
+    "return_attn_probs": False,
+}
+
+
+def _check_options(name: str, causal: bool, options: dict) -> None:
+    if not causal:
+        raise NotImplementedError(f"{name}: only causal attention is implemented "
+                                  "(the reference always passes causal=True)")
+    for key, value in options.items():
+        if key not in _UNSUPPORTED_DEFAULTS:
+            raise TypeError(f"{name}: unexpected argument {key!r}")
+        if value != _UNSUPPORTED_DEFAULTS[key]:
+            raise NotImplementedError(f"{name}: {key}={value!r} is not supported")
+
+
+def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k,
+                           softmax_scale=None, causal=False, block_table=None, **options):
+    """Causal varlen attention (attention.py:105-116).  With ``block_table``
+    k and v are the paged caches [blocks, block_size, kv_heads, 128] and
+    request i reads the first cu_seqlens_k[i+1] - cu_seqlens_k[i] rows of its
+    table; without, k and v hold every request's keys back to back
+    [total_k, kv_heads, 128].  The queries of a request are the last ones of
+    its context (bottom-right causal alignment).  Returns [total_q, heads, 128]."""
+    _check_options("flash_attn_varlen_func", causal, options)
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
+    if block_table is None:
+        # Contiguous keys: a cache of one-row blocks whose table for request
+        # i counts up from cu_seqlens_k[i] (entries past its length are
+        # never read).
+        if k.ndim != 3 or v.shape != k.shape:
+            raise ValueError("without block_table, k and v must be [total_k, kv_heads, head_dim]")
+        k_cache = k.contiguous().unsqueeze(1)
+        v_cache = v.contiguous().unsqueeze(1)
+        width = max(1, int(max_seqlen_k))
+        columns = torch.arange(width, dtype=torch.int32, device=k.device)
+        block_table = (cu_seqlens_k[:-1].unsqueeze(1) + columns.unsqueeze(0)).contiguous()
+    else:
+        k_cache, v_cache = k, v
+    return _BACKEND.paged_attention_prefill(q, k_cache, v_cache, block_table, cu_seqlens_q,
+                                            cu_seqlens_k, scale)
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table=None,
+                            softmax_scale=None, causal=False, **options):
+    """One decode token per sequence over its paged context
+    (attention.py:122-130): q [batch, 1, heads, 128], caches [blocks,
+    block_size, kv_heads, 128], cache_seqlens [batch] int32 context lengths,
+    block_table [batch, width] int32.  Returns [batch, 1, heads, 128]."""
+    _check_options("flash_attn_with_kvcache", causal, options)
+    if q.ndim != 4 or q.shape[1] != 1:
+        raise NotImplementedError("flash_attn_with_kvcache: one query token per sequence only")
+    if cache_seqlens is None or block_table is None:
+        raise NotImplementedError("flash_attn_with_kvcache: needs cache_seqlens and block_table")
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
+    batch = q.shape[0]
+    lengths = cache_seqlens.to(device=q.device, dtype=torch.int32)
+    cu_seqlens_k = torch.zeros(batch + 1, dtype=torch.int32, device=q.device)
+    torch.cumsum(lengths, 0, out=cu_seqlens_k[1:])
+    # The plan is sized for the longest contexts the tables can hold, so the
+    # lengths are not read back to the host (unless the synchronising index
+    # checks are on, which compare the exact total).
+    if index_value_validation_enabled(lengths):
+        total = int(cu_seqlens_k[-1])
+    else:
+        total = batch * block_table.shape[1] * k_cache.shape[1]
+    out = _BACKEND.paged_attention_decode(q[:, 0], k_cache, v_cache, block_table, cu_seqlens_k,
+                                          total, scale)
+    return out.unsqueeze(1)

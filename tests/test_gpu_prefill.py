@@ -213,3 +213,72 @@ def test_chunked_prefill_full_size(backend, gpu_device):
     scale = 1 / math.sqrt(128)
     out = run(backend, dev, scale)
     check_close(out, *reference(host, scale), "chunked prefill")
+
+
+# ------------------------------------------------ flash-attn call drop-ins
+
+def test_flash_varlen_with_block_table_matches_oracle(gpu_device):
+    """attention.py:105-116: flash_attn_varlen_func(q, k_cache, v_cache,
+    ..., causal=True, block_table=...)."""
+    from nanokv.flash import flash_attn_varlen_func
+
+    q_lens, k_lens = [37, 1, 130], [300, 9, 130]
+    dev, host = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=23)
+    out = flash_attn_varlen_func(dev["q"], dev["kc"], dev["vc"], max_seqlen_q=max(q_lens),
+                                 cu_seqlens_q=dev["cu_q"], max_seqlen_k=max(k_lens),
+                                 cu_seqlens_k=dev["cu_k"], softmax_scale=0.09, causal=True,
+                                 block_table=dev["tables"])
+    check_close(out, *reference(host, 0.09), "flash varlen paged")
+
+
+def test_flash_varlen_contiguous_keys_matches_oracle(gpu_device):
+    """The reference's prefill without block tables passes the step's own
+    k and v (views of the QKV projection) back to back."""
+    from nanokv.flash import flash_attn_varlen_func
+
+    q_lens = [70, 5, 129]
+    dev, host = build_case(gpu_device, 4, 2, 16, q_lens, q_lens, seed=31)
+    total = sum(q_lens)
+    k_rows = np.concatenate([oracle.gather(host["kc"], host["tables"][i], n) for i, n in enumerate(q_lens)])
+    v_rows = np.concatenate([oracle.gather(host["vc"], host["tables"][i], n) for i, n in enumerate(q_lens)])
+    qkv = torch.zeros((total, 16 * 128), dtype=torch.bfloat16, device=gpu_device)
+    k = qkv[:, 8 * 128:12 * 128].view(total, 4, 128)  # strided views, as after the QKV split
+    v = qkv[:, 12 * 128:].view(total, 4, 128)
+    k.copy_(torch.from_numpy(k_rows).view(torch.bfloat16).to(gpu_device))
+    v.copy_(torch.from_numpy(v_rows).view(torch.bfloat16).to(gpu_device))
+    out = flash_attn_varlen_func(dev["q"], k, v, max(q_lens), dev["cu_q"], max(q_lens), dev["cu_q"],
+                                 softmax_scale=0.1, causal=True)
+    check_close(out, *reference(host, 0.1), "flash varlen contiguous")
+
+
+def test_flash_with_kvcache_matches_decode_oracle(gpu_device):
+    """attention.py:122-130: flash_attn_with_kvcache(q.unsqueeze(1), k_cache,
+    v_cache, cache_seqlens=context_lens, block_table=..., causal=True)."""
+    from nanokv.flash import flash_attn_with_kvcache
+
+    k_lens = [1, 300, 17, 64]
+    dev, host = build_case(gpu_device, 8, 2, 16, [1] * 4, k_lens, seed=37)
+    lens = torch.tensor(k_lens, dtype=torch.int32, device=gpu_device)
+    out = flash_attn_with_kvcache(dev["q"].unsqueeze(1), dev["kc"], dev["vc"], cache_seqlens=lens,
+                                  block_table=dev["tables"], softmax_scale=0.088, causal=True)
+    assert out.shape == (4, 1, 16, 128)
+    ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], host["tables"],
+                                        np.array(k_lens), 0.088)
+    g = out[:, 0].float().cpu().numpy()
+    assert not (np.abs(g - ref) > 1e-3 + 1e-2 * np.abs(ref)).any()
+
+
+def test_flash_dropins_reject_what_they_do_not_compute(gpu_device):
+    from nanokv.flash import flash_attn_varlen_func, flash_attn_with_kvcache
+
+    dev, _ = build_case(gpu_device, 8, 2, 16, [4], [4], seed=2)
+    with pytest.raises(NotImplementedError):
+        flash_attn_varlen_func(dev["q"], dev["kc"], dev["vc"], 4, dev["cu_q"], 4, dev["cu_k"],
+                               causal=False, block_table=dev["tables"])
+    with pytest.raises(NotImplementedError):
+        flash_attn_varlen_func(dev["q"], dev["kc"], dev["vc"], 4, dev["cu_q"], 4, dev["cu_k"],
+                               causal=True, block_table=dev["tables"], window_size=(8, 0))
+    with pytest.raises(TypeError):
+        flash_attn_with_kvcache(dev["q"][:1].unsqueeze(1), dev["kc"], dev["vc"],
+                                cache_seqlens=dev["cu_k"][1:], block_table=dev["tables"],
+                                causal=True, rotary_cos=None)
