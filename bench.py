@@ -25,7 +25,9 @@ gather over contiguous block tables; "other_workloads" times the
 single-layer store / gather configurations (decode store, chunked-prefill
 store, prefix-cache gather, narrow rows) kernel by kernel; "gpu_reference"
 runs the reference pytorch backend's torch ops on the same GPU, on the
-decode step and on the reference's own store/gather microbenchmark matrix.
+decode step and on the reference's own store/gather microbenchmark matrix;
+"prefill_attention" times the causal paged prefill kernel on the
+chunked-prefill step against the reference's SDPA prefill path.
 """
 from __future__ import annotations
 
@@ -79,6 +81,9 @@ def parse_args(argv=None):
                    help="skip the torch restatement of the reference pytorch backend on the GPU")
     p.add_argument("--profile", action="store_true",
                    help="run warmup + timed steps only (no check, no CPU baseline), for rocprofv3")
+    p.add_argument("--prefill-only", action="store_true",
+                   help="only time the paged prefill attention on the chunked-prefill step "
+                        "(and its SDPA-path baseline), print that record, then exit")
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="only run a plain device copy of this many MiB 3 times (the known-size "
                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
@@ -118,6 +123,9 @@ def main(argv=None) -> int:
         print(json.dumps({"copy_calibration_bytes": n, "launches": 3}), flush=True)
         return 0
     backend = create_paged_kv_backend("hip")
+    if args.prefill_only:
+        print(json.dumps(measure_prefill_attention(device, backend, args.steps)), flush=True)
+        return 0
 
     wl = workloads.build("decode_step", num_layers=args.layers)
     L, B = wl.num_layers, wl.num_seqs
@@ -231,6 +239,13 @@ def main(argv=None) -> int:
     block_pool = measure_block_pool(wl, device, packer, batch, args.steps, args.warmup)
     log(f"[bench] block pool: apply {block_pool['apply_kernel_us']:.1f} us, step "
         f"{block_pool['stream_us_per_step']:.1f} us stream / {block_pool['host_us_per_step']:.1f} us host")
+
+    prefill_attention = None
+    if not args.profile:
+        prefill_attention = measure_prefill_attention(device, backend, args.steps)
+        log(f"[bench] prefill attention (chunked prefill, 8192 tokens): "
+            f"{prefill_attention['us']:.1f} us, {prefill_attention['tflops']:.0f} TFLOP/s, "
+            f"torch SDPA path {prefill_attention['torch_sdpa_path_us']:.0f} us")
 
     gpu_reference = None
     if args.gpu_reference and not args.profile:
@@ -352,6 +367,7 @@ def main(argv=None) -> int:
         },
         "copy_reference": copy_reference,
         "other_workloads": other_workloads,
+        "prefill_attention": prefill_attention,
         "gpu_reference": gpu_reference,
         "block_pool": block_pool,
         "cpu_baseline": cpu_baseline,
@@ -360,6 +376,102 @@ def main(argv=None) -> int:
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+MI355X_BF16_DENSE_TFLOPS = 2500.0
+
+
+def chunked_prefill_shape(seed: int = 17):
+    """16 requests in one 8192-token chunk, lengths uniform in [128, 4096]
+    scaled to the chunk; requests 0-7 continue after 1-4 cached 256-row
+    blocks.  Returns (query lengths, context lengths)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(128, 4097, 16).astype(np.float64)
+    q_lens = np.floor(raw / raw.sum() * 8192).astype(np.int64)
+    q_lens[-1] += 8192 - q_lens.sum()
+    cached = np.zeros(16, np.int64)
+    cached[:8] = rng.integers(1, 5, 8) * 256
+    return q_lens.tolist(), (q_lens + cached).tolist()
+
+
+def measure_prefill_attention(device, backend, reps: int) -> dict:
+    """Causal prefill attention read straight from the paged cache (the
+    Flash path's prefill call) on the chunked-prefill step: Qwen3-VL-2B's 16
+    query heads over 8 kv heads, 256-row blocks.  Algorithmic FLOPs = 4 x
+    head_dim x query heads x the (query, visible key) pairs.  Beside it, the
+    reference's SDPA prefill on the same GPU: per request, the
+    pytorch-backend gathers of K and V and SDPA with the prefix-causal mask
+    (nanovllm/layers/attention.py:226-282)."""
+    import numpy as np
+    import torch
+
+    from nanokv.benchmark import LaunchTimer
+
+    q_lens, k_lens = chunked_prefill_shape()
+    hkv, g, bs, dim = 8, 2, 256, 128
+    need = [-(-k // bs) for k in k_lens]
+    nb = sum(need) + 4
+    gen = torch.Generator(device=device).manual_seed(19)
+    kc = torch.randn((nb, bs, hkv, dim), device=device, generator=gen).to(torch.bfloat16)
+    vc = torch.randn_like(kc)
+    perm = torch.randperm(nb, device=device, generator=gen).to(torch.int32)
+    tables = torch.full((len(q_lens), max(need)), -1, dtype=torch.int32, device=device)
+    offset = 0
+    for i, n in enumerate(need):
+        tables[i, :n] = perm[offset:offset + n]
+        offset += n
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32, device=device)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(k_lens)]), dtype=torch.int32, device=device)
+    q = torch.randn((sum(q_lens), hkv * g, dim), device=device, generator=gen).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(dim)
+    plan = backend.build_prefill_plan(q, kc, cu_q)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream(device)
+    timer = LaunchTimer(stream)
+    for i in range(reps + 3):
+        t0 = timer.start() if i >= 3 else None
+        backend.paged_attention_prefill(q, kc, vc, tables, cu_q, cu_k, scale, plan=plan, out=out)
+        if t0 is not None:
+            timer.stop(t0)
+    us = float(np.mean(timer.durations_us()))
+    pairs = sum(sum(lk - lq + j + 1 for j in range(lq)) for lq, lk in zip(q_lens, k_lens))
+    flops = 4 * dim * hkv * g * pairs
+    ref = torch_reference_backend()
+
+    def sdpa_path():
+        for i, (lq, lk) in enumerate(zip(q_lens, k_lens)):
+            k = ref.gather(kc, tables[i], lk)
+            v = ref.gather(vc, tables[i], lk)
+            query = q[int(cu_q[i]):int(cu_q[i + 1])]
+            visible = (torch.arange(lk, device=device)[None, :]
+                       <= (torch.arange(lq, device=device) + (lk - lq))[:, None])
+            torch.nn.functional.scaled_dot_product_attention(
+                query.transpose(0, 1).unsqueeze(0), k.transpose(0, 1).unsqueeze(0).contiguous(),
+                v.transpose(0, 1).unsqueeze(0).contiguous(), attn_mask=visible[None, None],
+                scale=scale, enable_gqa=True)
+
+    sdpa_path()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        sdpa_path()
+    torch.cuda.synchronize()
+    sdpa_us = (time.perf_counter() - t0) / 3 * 1e6
+    return {
+        "workload": "chunked prefill: 16 requests, 8192 query tokens, 8 continuing after 1-4 "
+                    "cached blocks; 16 query heads over 8 kv heads, head_dim 128, 256-row blocks",
+        "kernel": "attn_prefill_kernel<2> (MFMA 16x16x32 bf16, causal, paged)",
+        "us": round(us, 2),
+        "algorithmic_flops": flops,
+        "tflops": round(flops / us / 1e6, 1),
+        "peak_tflops": MI355X_BF16_DENSE_TFLOPS,
+        "frac": round(flops / us / 1e6 / MI355X_BF16_DENSE_TFLOPS, 4),
+        "bound": "mfma",
+        "torch_sdpa_path_us": round(sdpa_us, 1),
+        "speedup_vs_torch_sdpa_path": round(sdpa_us / us, 2),
+    }
 
 
 OTHER_WORKLOADS = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows")
