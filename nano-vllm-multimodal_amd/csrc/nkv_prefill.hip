@@ -261,13 +261,17 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
 
   const int32_t num_tiles = (num_keys + kPfKeys - 1) / kPfKeys;
   float row_max[2] = {-INFINITY, -INFINITY};
-  float row_sum[2] = {0.f, 0.f};  // this lane's share of the row's weight sum
-  f32x4 acc[8][2];                // O^T blocks: dims 16 * db + 4 * g4 + i, row m
+  // O^T blocks: dims 16 * db + 4 * g4 + i of row m.  Block 8 multiplies P
+  // by a row of ones (dim 128 of an extended V^T), so its first dim holds
+  // the row's weight sum, taken from the same bf16 weights as the output.
+  f32x4 acc[9][2];
 #pragma unroll
-  for (int db = 0; db < 8; ++db) {
+  for (int db = 0; db < 9; ++db) {
     acc[db][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const __bf16 one = c16 == 0 ? static_cast<__bf16>(1.f) : static_cast<__bf16>(0.f);
+  const bf16x8 ones = {one, one, one, one, one, one, one, one};
 
   // Rows are resolved two tiles ahead (slots rotate over 3); the copies of
   // tile t + 1 are in flight while tile t is computed.
@@ -346,9 +350,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
       if (__any(move)) {
         const float m_new = move ? local : row_max[mb];
         const float alpha = move ? __builtin_amdgcn_exp2f(row_max[mb] - m_new) : 1.f;
-        row_sum[mb] *= alpha;  // alpha = 0 when the old reference was -inf
 #pragma unroll
-        for (int db = 0; db < 8; ++db) acc[db][mb] *= alpha;
+        for (int db = 0; db < 9; ++db) acc[db][mb] *= alpha;  // 0 when the old reference was -inf
         row_max[mb] = m_new;
       }
       // A row with nothing visible yet keeps the reference -inf: its
@@ -360,7 +363,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           p[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][mb][i], scale_log2, -ref));
-          row_sum[mb] += p[kb][i];
         }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -390,13 +392,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
         acc[db][1] = mfma(a, pb[c][1], acc[db][1]);
       }
     }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      acc[8][0] = mfma(ones, pb[c][0], acc[8][0]);
+      acc[8][1] = mfma(ones, pb[c][1], acc[8][1]);
+    }
     slot = slot1;
   }
 
-  // Normalise and store: the row's weight sum is spread over its 4 lanes.
+  // Normalise and store: the row's weight sum sits in the g4 == 0 lane.
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
-    const float total = row4_sum(row_sum[mb]);
+    const float total = row4_sum(g4 == 0 ? acc[8][mb][0] : 0.f);
     const int m = wave * 32 + mb * 16 + c16;
     const int t = m / G;
     if (t >= ntok) continue;
