@@ -28,13 +28,20 @@
 // Invalid block ids (outside [0, num_blocks), or past the table) drop their
 // keys, as in the decode kernel.
 #include <cmath>
+#include <type_traits>
 
 #include "nkv_common.h"
 
 namespace nkv {
 namespace {
 
-constexpr int kPfWaves = 4;
+#ifndef NKV_PF_WAVES
+#define NKV_PF_WAVES 4  // wavefronts per workgroup (4 or 8), 32 query rows each
+#endif
+constexpr int kPfWaves = NKV_PF_WAVES;
+static_assert(kPfWaves == 4 || kPfWaves == 8, "NKV_PF_WAVES must be 4 or 8");
+// Two wavefronts per SIMD: two 4-wave workgroups per CU, or one of 8.
+constexpr int kPfBlocksPerCU = 8 / kPfWaves;
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfRows = kPfWaves * 32;  // query rows per workgroup
 constexpr int kPfKeys = 64;             // keys per tile
@@ -64,12 +71,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // conflict-free:
 //   K: chunk c at c ^ (r % 16)    (ds_read_b128: 16 keys at one chunk)
 //   V: chunk c at c ^ 2 (r % 8)   (ds_read_b64_tr_b16: 16 keys x 32 bytes)
-struct PrefillShared {
-  u32x4 k[2][kPfKeys * 16];
-  u32x4 v[2][kPfKeys * 16];
-  int32_t rows[3][kPfKeys];  // physical row of each key of a tile, -1 if invalid
-  int32_t invalid[3];        // whether a tile has an invalid row
-};
+// Each buffer is its own __shared__ array, and the loop body is compiled
+// once per buffer parity, so the compiler can tell the tile being read from
+// the one being copied into and does not wait for the copies in flight.
+constexpr int kTileChunks = kPfKeys * 16;  // 16-byte chunks per K or V tile
 
 __device__ __forceinline__ int k_index(int key, int chunk) { return key * 16 + (chunk ^ (key & 15)); }
 __device__ __forceinline__ int v_index(int key, int chunk) {
@@ -142,51 +147,64 @@ struct ContextMap {
   int32_t num_keys;     // rows past this are never read
 
   // Physical cache row of context row t, or -1 when t is past num_keys or
-  // the table, or its block id is outside [0, num_blocks).
-  __device__ __forceinline__ int32_t row(int32_t t) const {
-    int32_t logical, offset;
-    if (block_shift >= 0) {
-      logical = t >> block_shift;
-      offset = t & (block_size - 1);
-    } else {
-      logical = t / block_size;
-      offset = t - logical * block_size;
-    }
+  // the table, or its block id is outside [0, num_blocks).  Split in two so
+  // that the table load can be issued early and consumed late.
+  __device__ __forceinline__ int32_t block_of(int32_t t) const {
+    const int32_t logical = block_shift >= 0 ? t >> block_shift : t / block_size;
     if (t >= num_keys || logical >= table_stride) return -1;
-    const int32_t block = table[logical];
+    return table[logical];
+  }
+  __device__ __forceinline__ int32_t row_in(int32_t t, int32_t block) const {
     if (block < 0 || block >= num_blocks) return -1;
+    const int32_t offset = block_shift >= 0 ? t & (block_size - 1) : t % block_size;
     return block * block_size + offset;  // num_blocks * block_size <= INT32_MAX
   }
+  __device__ __forceinline__ int32_t row(int32_t t) const { return row_in(t, block_of(t)); }
 };
 
 // Wavefront 0 resolves the 64 rows of the tile starting at key0 (one per
-// lane) and whether any of them is invalid.
-__device__ __forceinline__ void resolve_rows(PrefillShared& sh, int slot, const ContextMap& map,
-                                             int32_t key0, int lane) {
-  const int32_t row = map.row(key0 + lane);
-  sh.rows[slot][lane] = row;
+// lane, from the block id its lane loaded) and whether any is invalid.
+__device__ __forceinline__ void resolve_rows(int32_t* rows, int32_t* invalid, const ContextMap& map,
+                                             int32_t key0, int32_t block, int lane) {
+  const int32_t row = map.row_in(key0 + lane, block);
+  rows[lane] = row;
   const bool any_invalid = __any(row < 0);
-  if (lane == 0) sh.invalid[slot] = any_invalid ? 1 : 0;
+  if (lane == 0) *invalid = any_invalid ? 1 : 0;
 }
 
-// This wavefront's share of one tile's copies: keys 16 w .. 16 w + 15, K
-// and V, 4 keys per instruction.  An invalid row reads the start of the
+// One wavefront copies 16 bytes per lane from global memory straight into
+// LDS: lane l's bytes land at lds_dst + 16 l (global_load_lds_dwordx4, LDS
+// base in M0).  Written as asm so that the compiler, which cannot tell which
+// LDS buffer such a copy writes, does not make every later LDS access wait
+// for it: the kernel waits for its copies itself (s_waitcnt, then a barrier)
+// before it reads the buffer they fill.
+__device__ __forceinline__ void lds_copy16(const uint8_t* src, u32x4* lds_dst) {
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u32x4*)lds_dst)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(base)
+               : "m0", "memory");
+}
+
+// This wavefront's share of one tile's copies: 64 / waves consecutive keys,
+// K and V, 4 keys per instruction.  An invalid row reads the start of the
 // cache instead (in bounds); its K scores are masked and its V zeroed.
-__device__ __forceinline__ void issue_tile(PrefillShared& sh, int buf, const int32_t* rows,
+__device__ __forceinline__ void issue_tile(u32x4* k_dst, u32x4* v_dst, const int32_t* rows,
                                            const uint8_t* key_cache, const uint8_t* value_cache,
                                            int64_t row_bytes, int64_t head_bytes, int wave,
                                            int lane) {
+  constexpr int kKeysPerWave = kPfKeys / kPfWaves;
   const int pos = lane & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key0 = 16 * wave + 4 * i;
+  for (int i = 0; i < kKeysPerWave / 4; ++i) {
+    const int key0 = kKeysPerWave * wave + 4 * i;
     const int key = key0 + (lane >> 4);
     const int32_t row = rows[key];
     const int64_t base = row >= 0 ? row * row_bytes + head_bytes : 0;
-    __builtin_amdgcn_global_load_lds(key_cache + base + 16 * (pos ^ (key & 15)),
-                                     &sh.k[buf][key0 * 16], 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(value_cache + base + 16 * (pos ^ ((key & 7) << 1)),
-                                     &sh.v[buf][key0 * 16], 16, 0, 0);
+    lds_copy16(key_cache + base + 16 * (pos ^ (key & 15)), k_dst + key0 * 16);
+    lds_copy16(value_cache + base + 16 * (pos ^ ((key & 7) << 1)), v_dst + key0 * 16);
   }
 }
 
@@ -194,17 +212,17 @@ __device__ __forceinline__ void issue_tile(PrefillShared& sh, int buf, const int
 // supplies the address of V[key][dim4 .. +4] and receives, as lane 16 G + i,
 // V[key of lane 16 G + 4 j'][dim of lane 16 G + i] for j' = 0..3 (the
 // gfx950 transposing LDS read).
-__device__ __forceinline__ u32x2 v_tr_read(const PrefillShared& sh, int buf, int key, int dim4) {
+__device__ __forceinline__ u32x2 v_tr_read(const u32x4* v_tile, int key, int dim4) {
   const int byte = (v_index(key, dim4 >> 3) << 4) + ((dim4 & 7) << 1);
   typedef short v4i16 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) char lds_char;
   typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-  lds_v4i16* p = (lds_v4i16*)((lds_char*)(&sh.v[buf][0]) + byte);  // generic -> LDS
+  lds_v4i16* p = (lds_v4i16*)((lds_char*)(v_tile) + byte);  // generic -> LDS
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
 
 template <int G>
-__global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
+__global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_token_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
     const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,
@@ -213,7 +231,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
     const int4* __restrict__ plan, int32_t num_seqs, float scale_log2,
     uint16_t* __restrict__ out, int64_t out_token_stride) {
   constexpr int kTileTokens = kPfRows / G;
-  __shared__ PrefillShared sh;
+  __shared__ u32x4 k_buf0[kTileChunks];
+  __shared__ u32x4 k_buf1[kTileChunks];
+  __shared__ u32x4 v_buf0[kTileChunks];
+  __shared__ u32x4 v_buf1[kTileChunks];
+  __shared__ int32_t rows_buf[3][kPfKeys];  // physical row of each key of a tile, -1 if invalid
+  __shared__ int32_t invalid_buf[3];        // whether a tile has an invalid row
 
   const int4 entry = plan[blockIdx.x];
   const int32_t seq = entry.x;
@@ -276,33 +299,50 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
   // Rows are resolved two tiles ahead (slots rotate over 3); the copies of
   // tile t + 1 are in flight while tile t is computed.
   if (wave == 0) {
-    resolve_rows(sh, 0, map, 0, lane);
-    if (num_tiles > 1) resolve_rows(sh, 1, map, kPfKeys, lane);
+    resolve_rows(rows_buf[0], &invalid_buf[0], map, 0, map.block_of(lane), lane);
+    if (num_tiles > 1) {
+      resolve_rows(rows_buf[1], &invalid_buf[1], map, kPfKeys, map.block_of(kPfKeys + lane), lane);
+    }
   }
   __syncthreads();
-  issue_tile(sh, 0, sh.rows[0], key_cache, value_cache, row_bytes, head_bytes, wave, lane);
+  issue_tile(k_buf0, v_buf0, rows_buf[0], key_cache, value_cache, row_bytes, head_bytes, wave,
+             lane);
   int slot = 0;  // rows slot of the current tile
-  for (int32_t tile = 0; tile < num_tiles; ++tile) {
+  const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses in a V^T read, within 16
+  const int tr_dim = 4 * (lane & 3);              // first dim it addresses, within 16
+
+  auto tile_step = [&](auto parity, int32_t tile) {
+    constexpr int kCur = decltype(parity)::value;
+    u32x4* const k_cur = kCur == 0 ? k_buf0 : k_buf1;
+    u32x4* const v_cur = kCur == 0 ? v_buf0 : v_buf1;
+    u32x4* const k_next = kCur == 0 ? k_buf1 : k_buf0;
+    u32x4* const v_next = kCur == 0 ? v_buf1 : v_buf0;
     const int32_t key0 = tile * kPfKeys;
-    const int cur = tile & 1;
     const int slot1 = slot == 2 ? 0 : slot + 1;
     const int slot2 = slot1 == 2 ? 0 : slot1 + 1;
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of the tile have landed
     __syncthreads();                // ... and everyone's; the previous tile is consumed
-    const bool has_invalid = sh.invalid[slot] != 0;
+    const bool has_invalid = invalid_buf[slot] != 0;
     if (has_invalid) {  // zero V of invalid rows (what the cache start held may be anything)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kTileChunks / kPfThreads; ++i) {
         const int idx = i * kPfThreads + tid;
-        if (sh.rows[slot][idx >> 4] < 0) sh.v[cur][idx] = u32x4{0u, 0u, 0u, 0u};
+        if (rows_buf[slot][idx >> 4] < 0) v_cur[idx] = u32x4{0u, 0u, 0u, 0u};
       }
       __syncthreads();
     }
+    // Wavefront 0 resolves the rows of tile t + 2 before the copies of tile
+    // t + 1 are issued: its wait for the block ids then has nothing else to
+    // wait for (a vector-memory wait covers every older load, copies
+    // included).
+    if (wave == 0 && tile + 2 < num_tiles) {
+      resolve_rows(rows_buf[slot2], &invalid_buf[slot2], map, key0 + 2 * kPfKeys,
+                   map.block_of(key0 + 2 * kPfKeys + lane), lane);
+    }
     if (tile + 1 < num_tiles) {
-      issue_tile(sh, cur ^ 1, sh.rows[slot1], key_cache, value_cache, row_bytes, head_bytes,
+      issue_tile(k_next, v_next, rows_buf[slot1], key_cache, value_cache, row_bytes, head_bytes,
                  wave, lane);
     }
-    if (wave == 0 && tile + 2 < num_tiles) resolve_rows(sh, slot2, map, key0 + 2 * kPfKeys, lane);
     // A tile is plain when every row sees all its keys and all are valid:
     // its scores need no mask.
     const bool plain = !has_invalid && key0 + kPfKeys <= first_row_keys;
@@ -315,7 +355,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
       st[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) {
-        const bf16x8 a = as_bf16x8(sh.k[cur][k_index(16 * kb + c16, 4 * dc + g4)]);
+        const bf16x8 a = as_bf16x8(k_cur[k_index(16 * kb + c16, 4 * dc + g4)]);
         st[kb][0] = mfma(a, qb[0][dc], st[kb][0]);
         st[kb][1] = mfma(a, qb[1][dc], st[kb][1]);
       }
@@ -323,7 +363,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
 
     // Online softmax per row (exp2 units); P^T operands for both 32-key steps.
     bf16x8 pb[2][2];
-    const int4* rows_now = reinterpret_cast<const int4*>(sh.rows[slot]);
+    const int4* rows_now = reinterpret_cast<const int4*>(rows_buf[slot]);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       if (!plain) {  // hide keys past the row's limit or in invalid rows
@@ -379,14 +419,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
     // O^T += V^T P^T.  Step c covers keys 32 c .. +32 in the order the P^T
     // operand holds them: slots 0-3 = keys 32c + 4 g4 + j, slots 4-7 = keys
     // 32c + 16 + 4 g4 + j; the transposing reads deliver V^T in that order.
-    const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses, within 16
-    const int tr_dim = 4 * (lane & 3);              // first dim this lane addresses, within 16
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const u32x2 lo = v_tr_read(sh, cur, 32 * c + tr_key, 16 * db + tr_dim);
-        const u32x2 hi = v_tr_read(sh, cur, 32 * c + 16 + tr_key, 16 * db + tr_dim);
+        const u32x2 lo = v_tr_read(v_cur, 32 * c + tr_key, 16 * db + tr_dim);
+        const u32x2 hi = v_tr_read(v_cur, 32 * c + 16 + tr_key, 16 * db + tr_dim);
         const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
         acc[db][0] = mfma(a, pb[c][0], acc[db][0]);
         acc[db][1] = mfma(a, pb[c][1], acc[db][1]);
@@ -398,6 +436,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void attn_prefill_kernel(
       acc[8][1] = mfma(ones, pb[c][1], acc[8][1]);
     }
     slot = slot1;
+  };
+  for (int32_t tile = 0; tile < num_tiles; tile += 2) {
+    tile_step(std::integral_constant<int, 0>{}, tile);
+    if (tile + 1 < num_tiles) tile_step(std::integral_constant<int, 1>{}, tile + 1);
   }
 
   // Normalise and store: the row's weight sum sits in the g4 == 0 lane.

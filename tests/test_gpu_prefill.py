@@ -103,7 +103,7 @@ def test_plan_tiles_cover_every_query(backend, gpu_device):
     q_lens, k_lens = [200, 1, 0, 64, 65], [300, 5, 3, 64, 65]
     dev, host = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=3)
     tile = int(_lib.load_library().nkv_prefill_tile_tokens(2))
-    assert tile == 64
+    assert tile in (64, 128)  # 128 or 256 query rows per workgroup, 2 heads per token
     plan = backend.build_prefill_plan(dev["q"], dev["kc"], dev["cu_q"]).cpu().numpy()
     expect = [-(-n // tile) for n in q_lens]
     entries = plan[: sum(expect)]
