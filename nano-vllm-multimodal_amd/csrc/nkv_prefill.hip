@@ -15,16 +15,18 @@
 //     (token, query head) pairs of 128 / G consecutive tokens and the
 //     G = Hq / Hkv query heads that share the kv head, token-major;
 //     each of its 4 waves owns 32 of those rows (two 16-row blocks);
-//   * the keys stream in tiles of 64: K is staged in LDS row-major, V
-//     transposed (4 x 8 blocks transposed in registers, then 8-byte LDS
-//     stores), both with padded rows;
+//   * the keys stream in tiles of 64, K and V copied straight from the cache
+//     into LDS (global_load_lds, swizzled 16-byte chunks), one tile in
+//     flight while the previous one is computed; the V^T operands come from
+//     the transposing LDS read of gfx950;
 //   * scores are computed transposed, S^T = K Q^T, so that a lane's
 //     accumulators all belong to ONE query row: the online softmax needs
 //     only a 4-lane max per row, the P^T operand of O^T = V^T P^T comes
-//     straight from the score registers (the key order inside each 32-key
-//     step is permuted identically in V^T), and the output rescale is a
-//     per-lane factor;
-//   * P is rounded to bf16 for the second product, as flash attention does.
+//     straight from the score registers (the transposing reads deliver V^T
+//     in the same key order), and the output rescale is a per-lane factor;
+//   * P is rounded to bf16 for the second product, as flash attention does,
+//     and the row sum is taken from the same bf16 weights;
+//   * the query tiles of one kv head run on one XCD (shared L2).
 // Invalid block ids (outside [0, num_blocks), or past the table) drop their
 // keys, as in the decode kernel.
 #include <cmath>
@@ -57,12 +59,6 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// K tile [key][dim], 256 B per key with the 16-byte chunks of key r stored
-// at chunk ^ (r % 16): an operand load (16 keys at one chunk) then touches
-// 16 different chunk positions.  V^T tile [dim][key], 128 B per dim with the
-// 8-byte units (4 keys) of dim d stored at unit ^ ((d ^ d / 8) % 16): the
-// operand loads (16 consecutive dims at one unit) hit 16 different units,
-// and the staging stores (dims 8 apart) at least 8.
 // K and V tiles, double-buffered, copied straight from global memory into
 // LDS by global_load_lds (one wavefront instruction fills 1 KiB of
 // consecutive LDS: 4 keys x 256 B; the source address of each lane picks
@@ -221,6 +217,35 @@ __device__ __forceinline__ u32x2 v_tr_read(const u32x4* v_tile, int key, int dim
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
 
+// Workgroups are handed to the 8 XCDs round-robin by linear id (id % 8), and
+// each XCD has its own L2.  The grid is one-dimensional and its ids are
+// mapped so that the query tiles of one kv head run on one XCD, or on 8 / H
+// of them when there are H < 8 kv heads: the tiles that read the same K/V
+// rows then share an L2 instead of each XCD fetching them again.  Within an
+// XCD the tiles keep the plan's order (each sequence's last tile first).
+//   layout 1 (H a multiple of 8): XCD x runs kv heads x, x + 8, ... in turn;
+//   layout 2 (H divides 8): XCD x runs kv head x / R, R = 8 / H, and every
+//     R-th plan entry from x % R; the grid is 8 ceil(capacity / R), and ids
+//     past the plan exit;
+//   layout 0 (any other H): kv head fastest, no XCD grouping.
+constexpr int kXcds = 8;
+struct TileId {
+  int32_t entry;    // plan entry
+  int32_t kv_head;
+};
+
+__device__ __forceinline__ TileId tile_of(uint32_t id, int32_t num_kv_heads, int32_t capacity,
+                                          int32_t layout) {
+  const int32_t x = static_cast<int32_t>(id % kXcds);
+  const int32_t turn = static_cast<int32_t>(id / kXcds);  // dispatch order within the XCD
+  if (layout == 1) return TileId{turn % capacity, x + kXcds * (turn / capacity)};
+  if (layout == 2) {
+    const int32_t per_head = kXcds / num_kv_heads;
+    return TileId{turn * per_head + x % per_head, x / per_head};
+  }
+  return TileId{static_cast<int32_t>(id / num_kv_heads), static_cast<int32_t>(id % num_kv_heads)};
+}
+
 template <int G>
 __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_token_stride,
@@ -228,8 +253,8 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
     const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,
     int32_t block_shift, int32_t num_blocks, int32_t num_kv_heads,
     const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
-    const int4* __restrict__ plan, int32_t num_seqs, float scale_log2,
-    uint16_t* __restrict__ out, int64_t out_token_stride) {
+    const int4* __restrict__ plan, int32_t capacity, int32_t xcd_layout, int32_t num_seqs,
+    float scale_log2, uint16_t* __restrict__ out, int64_t out_token_stride) {
   constexpr int kTileTokens = kPfRows / G;
   __shared__ u32x4 k_buf0[kTileChunks];
   __shared__ u32x4 k_buf1[kTileChunks];
@@ -238,11 +263,13 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
   __shared__ int32_t rows_buf[3][kPfKeys];  // physical row of each key of a tile, -1 if invalid
   __shared__ int32_t invalid_buf[3];        // whether a tile has an invalid row
 
-  const int4 entry = plan[blockIdx.x];
+  const TileId id = tile_of(blockIdx.x, num_kv_heads, capacity, xcd_layout);
+  if (id.entry >= capacity) return;
+  const int4 entry = plan[id.entry];
   const int32_t seq = entry.x;
   const int32_t tok0 = entry.y;
   const int32_t ntok = entry.z;
-  const int32_t kh = blockIdx.y;
+  const int32_t kh = id.kv_head;
   // Uniform exits for empty or malformed entries.
   if (ntok <= 0 || ntok > kTileTokens || seq < 0 || seq >= num_seqs || tok0 < 0) return;
   const int32_t q_begin = cu_seqlens_q[seq];
@@ -296,13 +323,16 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
   const __bf16 one = c16 == 0 ? static_cast<__bf16>(1.f) : static_cast<__bf16>(0.f);
   const bf16x8 ones = {one, one, one, one, one, one, one, one};
 
-  // Rows are resolved two tiles ahead (slots rotate over 3); the copies of
-  // tile t + 1 are in flight while tile t is computed.
+  // Rows are resolved two tiles ahead (slots rotate over 3) from block ids
+  // loaded one tile before that; the copies of tile t + 1 are in flight
+  // while tile t is computed.
+  int32_t ahead_block = -1;  // wavefront 0: block id of its lane's key in the next tile to resolve
   if (wave == 0) {
     resolve_rows(rows_buf[0], &invalid_buf[0], map, 0, map.block_of(lane), lane);
     if (num_tiles > 1) {
       resolve_rows(rows_buf[1], &invalid_buf[1], map, kPfKeys, map.block_of(kPfKeys + lane), lane);
     }
+    if (num_tiles > 2) ahead_block = map.block_of(2 * kPfKeys + lane);
   }
   __syncthreads();
   issue_tile(k_buf0, v_buf0, rows_buf[0], key_cache, value_cache, row_bytes, head_bytes, wave,
@@ -331,13 +361,13 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
       }
       __syncthreads();
     }
-    // Wavefront 0 resolves the rows of tile t + 2 before the copies of tile
-    // t + 1 are issued: its wait for the block ids then has nothing else to
-    // wait for (a vector-memory wait covers every older load, copies
-    // included).
+    // Wavefront 0 resolves the rows of tile t + 2 from block ids that landed
+    // with the wait above, and loads those of tile t + 3, which land with
+    // the next tile's wait: no wait for the block table on the way.
     if (wave == 0 && tile + 2 < num_tiles) {
-      resolve_rows(rows_buf[slot2], &invalid_buf[slot2], map, key0 + 2 * kPfKeys,
-                   map.block_of(key0 + 2 * kPfKeys + lane), lane);
+      resolve_rows(rows_buf[slot2], &invalid_buf[slot2], map, key0 + 2 * kPfKeys, ahead_block,
+                   lane);
+      if (tile + 3 < num_tiles) ahead_block = map.block_of(key0 + 3 * kPfKeys + lane);
     }
     if (tile + 1 < num_tiles) {
       issue_tile(k_next, v_next, rows_buf[slot1], key_cache, value_cache, row_bytes, head_bytes,
@@ -464,8 +494,8 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
 
 using PrefillKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const uint8_t*,
                                const int32_t*, int64_t, int32_t, int32_t, int32_t, int32_t,
-                               const int32_t*, const int32_t*, const int4*, int32_t, float,
-                               uint16_t*, int64_t);
+                               const int32_t*, const int32_t*, const int4*, int32_t, int32_t,
+                               int32_t, float, uint16_t*, int64_t);
 
 PrefillKernel prefill_kernel_for(int64_t group) {
   switch (group) {
@@ -577,13 +607,27 @@ extern "C" int nkv_paged_attention_prefill(
     block_shift = 0;
     while ((int64_t{1} << block_shift) < block_size) ++block_shift;
   }
-  kernel<<<dim3(static_cast<unsigned>(capacity), static_cast<unsigned>(num_kv_heads)),
-           dim3(kPfThreads), 0, static_cast<hipStream_t>(stream)>>>(
+  int32_t xcd_layout = 0;
+  int64_t grid = capacity * num_kv_heads;
+  if (num_kv_heads % kXcds == 0) {
+    xcd_layout = 1;
+  } else if (kXcds % num_kv_heads == 0) {
+    xcd_layout = 2;
+    const int64_t per_head = kXcds / num_kv_heads;
+    grid = kXcds * ((capacity + per_head - 1) / per_head);
+  }
+  if (grid > static_cast<int64_t>(UINT32_MAX / kPfThreads)) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: %lld query tiles x %lld kv heads "
+                    "exceed one launch", static_cast<long long>(capacity),
+                    static_cast<long long>(num_kv_heads));
+  }
+  kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kPfThreads), 0,
+           static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(q), q_token_stride, static_cast<const uint8_t*>(key_cache),
       static_cast<const uint8_t*>(value_cache), block_tables, table_stride,
       static_cast<int32_t>(block_size), block_shift, static_cast<int32_t>(num_blocks),
       static_cast<int32_t>(num_kv_heads), cu_seqlens_q, cu_seqlens_k,
-      static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2,
-      static_cast<uint16_t*>(out), out_token_stride);
+      static_cast<const int4*>(plan), static_cast<int32_t>(capacity), xcd_layout,
+      static_cast<int32_t>(num_seqs), scale_log2, static_cast<uint16_t*>(out), out_token_stride);
   return nkv_check_launch("nkv_paged_attention_prefill");
 }
