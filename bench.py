@@ -430,12 +430,22 @@ def measure_prefill_attention(device, backend, reps: int) -> dict:
     out = torch.empty_like(q)
     stream = torch.cuda.current_stream(device)
     timer = LaunchTimer(stream)
-    for i in range(reps + 3):
-        t0 = timer.start() if i >= 3 else None
+
+    def launch():
         backend.paged_attention_prefill(q, kc, vc, tables, cu_q, cu_k, scale, plan=plan, out=out)
-        if t0 is not None:
-            timer.stop(t0)
-    us = float(np.mean(timer.durations_us()))
+
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    # One event pair around back-to-back launches: the host enqueues a call
+    # faster than the kernel runs, so the stream never idles and the mean is
+    # the kernel's duration (per-launch pairs would also count the time the
+    # idle stream waits for the host's next call).
+    t0 = timer.start()
+    for _ in range(reps):
+        launch()
+    timer.stop(t0)
+    us = timer.durations_us()[0] / reps
     pairs = sum(sum(lk - lq + j + 1 for j in range(lq)) for lq, lk in zip(q_lens, k_lens))
     flops = 4 * dim * hkv * g * pairs
     ref = torch_reference_backend()

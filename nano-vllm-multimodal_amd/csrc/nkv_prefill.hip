@@ -174,33 +174,55 @@ __device__ __forceinline__ void resolve_rows(int32_t* rows, int32_t* invalid, co
 // LDS buffer such a copy writes, does not make every later LDS access wait
 // for it: the kernel waits for its copies itself (s_waitcnt, then a barrier)
 // before it reads the buffer they fill.
-__device__ __forceinline__ void lds_copy16(const uint8_t* src, u32x4* lds_dst) {
+// LDS byte address of a __shared__ array (a constant once inlined).
+__device__ __forceinline__ uint32_t lds_address(const u32x4* array) {
   typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-  const uint32_t base = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u32x4*)lds_dst)));
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_u32x4*)array));
+}
+// Source as a 64-bit per-lane address; lds_dst is wave-uniform.
+__device__ __forceinline__ void lds_copy16(const uint8_t* src, uint32_t lds_dst) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                :
-               : "v"(src), "s"(base)
+               : "v"(src), "s"(lds_dst)
+               : "m0", "memory");
+}
+// Source as a wave-uniform base (SGPRs) plus a per-lane 32-bit byte offset.
+__device__ __forceinline__ void lds_copy16(const uint8_t* base, uint32_t offset, uint32_t lds_dst) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(offset), "s"(base), "s"(lds_dst)
                : "m0", "memory");
 }
 
-// This wavefront's share of one tile's copies: 64 / waves consecutive keys,
-// K and V, 4 keys per instruction.  An invalid row reads the start of the
-// cache instead (in bounds); its K scores are masked and its V zeroed.
-__device__ __forceinline__ void issue_tile(u32x4* k_dst, u32x4* v_dst, const int32_t* rows,
-                                           const uint8_t* key_cache, const uint8_t* value_cache,
-                                           int64_t row_bytes, int64_t head_bytes, int wave,
-                                           int lane) {
+// This wavefront's share of the copies of one K or V tile: 64 / waves
+// consecutive keys, 4 keys per instruction; lane l copies 16-byte chunk
+// swizzle(l % 16) of key l / 16.  The block rows are read first, so the
+// copies issue back to back.  Lanes of invalid rows copy nothing (the K
+// scores of such keys are masked and their V zeroed).  kWide: byte offsets
+// into the cache may exceed 32 bits, so lanes form 64-bit addresses.
+template <bool kWide, bool kValue>
+__device__ __forceinline__ void issue_copies(const u32x4* dst, const int32_t* rows,
+                                             const uint8_t* head_base, uint32_t row_bytes,
+                                             int wave, int lane) {
   constexpr int kKeysPerWave = kPfKeys / kPfWaves;
+  constexpr int kCopies = kKeysPerWave / 4;
   const int pos = lane & 15;
+  int32_t row[kCopies];
 #pragma unroll
-  for (int i = 0; i < kKeysPerWave / 4; ++i) {
+  for (int i = 0; i < kCopies; ++i) row[i] = rows[kKeysPerWave * wave + 4 * i + (lane >> 4)];
+#pragma unroll
+  for (int i = 0; i < kCopies; ++i) {
     const int key0 = kKeysPerWave * wave + 4 * i;
     const int key = key0 + (lane >> 4);
-    const int32_t row = rows[key];
-    const int64_t base = row >= 0 ? row * row_bytes + head_bytes : 0;
-    lds_copy16(key_cache + base + 16 * (pos ^ (key & 15)), k_dst + key0 * 16);
-    lds_copy16(value_cache + base + 16 * (pos ^ ((key & 7) << 1)), v_dst + key0 * 16);
+    const uint32_t chunk = 16u * (kValue ? pos ^ ((key & 7) << 1) : pos ^ (key & 15));
+    const uint32_t lds_dst = lds_address(dst) + key0 * 256;  // wave is uniform
+    if (row[i] >= 0) {
+      if (kWide) {
+        lds_copy16(head_base + static_cast<int64_t>(row[i]) * row_bytes + chunk, lds_dst);
+      } else {
+        lds_copy16(head_base, static_cast<uint32_t>(row[i]) * row_bytes + chunk, lds_dst);
+      }
+    }
   }
 }
 
@@ -246,7 +268,7 @@ __device__ __forceinline__ TileId tile_of(uint32_t id, int32_t num_kv_heads, int
   return TileId{static_cast<int32_t>(id / num_kv_heads), static_cast<int32_t>(id % num_kv_heads)};
 }
 
-template <int G>
+template <int G, bool kWide>
 __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_token_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
@@ -278,12 +300,13 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
   if (lk < lq || tok0 + ntok > lq) return;
 
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform: scalar registers
   const int lane = tid % kWave;
   const int c16 = lane & 15;  // the lane's query row inside a 16-row block
   const int g4 = lane >> 4;   // which quarter of the MFMA k dimension the lane holds
-  const int64_t row_bytes = static_cast<int64_t>(num_kv_heads) * kPfDim * 2;
-  const int64_t head_bytes = static_cast<int64_t>(kh) * kPfDim * 2;
+  const uint32_t row_bytes = static_cast<uint32_t>(num_kv_heads) * kPfDim * 2;
+  const uint8_t* const k_head = key_cache + static_cast<int64_t>(kh) * kPfDim * 2;
+  const uint8_t* const v_head = value_cache + static_cast<int64_t>(kh) * kPfDim * 2;
   // keys the last row sees (<= lk); every row sees at least first_row_keys
   const int32_t num_keys = lk - lq + tok0 + ntok;
   const int32_t first_row_keys = lk - lq + tok0 + 1;
@@ -335,8 +358,8 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
     if (num_tiles > 2) ahead_block = map.block_of(2 * kPfKeys + lane);
   }
   __syncthreads();
-  issue_tile(k_buf0, v_buf0, rows_buf[0], key_cache, value_cache, row_bytes, head_bytes, wave,
-             lane);
+  issue_copies<kWide, false>(k_buf0, rows_buf[0], k_head, row_bytes, wave, lane);
+  issue_copies<kWide, true>(v_buf0, rows_buf[0], v_head, row_bytes, wave, lane);
   int slot = 0;  // rows slot of the current tile
   const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses in a V^T read, within 16
   const int tr_dim = 4 * (lane & 3);              // first dim it addresses, within 16
@@ -353,7 +376,7 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of the tile have landed
     __syncthreads();                // ... and everyone's; the previous tile is consumed
     const bool has_invalid = invalid_buf[slot] != 0;
-    if (has_invalid) {  // zero V of invalid rows (what the cache start held may be anything)
+    if (has_invalid) {  // zero V of invalid rows (not copied: the buffer holds an older tile)
 #pragma unroll
       for (int i = 0; i < kTileChunks / kPfThreads; ++i) {
         const int idx = i * kPfThreads + tid;
@@ -369,10 +392,11 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
                    lane);
       if (tile + 3 < num_tiles) ahead_block = map.block_of(key0 + 3 * kPfKeys + lane);
     }
-    if (tile + 1 < num_tiles) {
-      issue_tile(k_next, v_next, rows_buf[slot1], key_cache, value_cache, row_bytes, head_bytes,
-                 wave, lane);
-    }
+    // The copies of tile t + 1 go out in two halves, K before the scores
+    // and V after them, rather than in one burst that every wavefront of
+    // the CU queues on at once.
+    const bool more = tile + 1 < num_tiles;
+    if (more) issue_copies<kWide, false>(k_next, rows_buf[slot1], k_head, row_bytes, wave, lane);
     // A tile is plain when every row sees all its keys and all are valid:
     // its scores need no mask.
     const bool plain = !has_invalid && key0 + kPfKeys <= first_row_keys;
@@ -390,6 +414,7 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
         st[kb][1] = mfma(a, qb[1][dc], st[kb][1]);
       }
     }
+    if (more) issue_copies<kWide, true>(v_next, rows_buf[slot1], v_head, row_bytes, wave, lane);
 
     // Online softmax per row (exp2 units); P^T operands for both 32-key steps.
     bf16x8 pb[2][2];
@@ -497,12 +522,13 @@ using PrefillKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const u
                                const int32_t*, const int32_t*, const int4*, int32_t, int32_t,
                                int32_t, float, uint16_t*, int64_t);
 
+template <bool kWide>
 PrefillKernel prefill_kernel_for(int64_t group) {
   switch (group) {
-    case 1: return attn_prefill_kernel<1>;
-    case 2: return attn_prefill_kernel<2>;
-    case 4: return attn_prefill_kernel<4>;
-    case 8: return attn_prefill_kernel<8>;
+    case 1: return attn_prefill_kernel<1, kWide>;
+    case 2: return attn_prefill_kernel<2, kWide>;
+    case 4: return attn_prefill_kernel<4, kWide>;
+    case 8: return attn_prefill_kernel<8, kWide>;
     default: return nullptr;
   }
 }
@@ -570,8 +596,7 @@ extern "C" int nkv_paged_attention_prefill(
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_prefill: num_q_heads must be a multiple of num_kv_heads");
   }
-  const PrefillKernel kernel = prefill_kernel_for(num_q_heads / num_kv_heads);
-  if (kernel == nullptr) {
+  if (nkv_prefill_tile_tokens(num_q_heads / num_kv_heads) == 0) {
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_prefill: %lld query heads per kv head (1, 2, 4 or 8 "
                     "supported)", static_cast<long long>(num_q_heads / num_kv_heads));
@@ -607,6 +632,12 @@ extern "C" int nkv_paged_attention_prefill(
     block_shift = 0;
     while ((int64_t{1} << block_shift) < block_size) ++block_shift;
   }
+  // Byte offsets of rows into one cache fit 32 bits unless the cache is
+  // larger than 4 GiB; then the copies form 64-bit addresses.
+  const int64_t row_bytes = num_kv_heads * head_dim * 2;
+  const bool wide = num_blocks * block_size * row_bytes > static_cast<int64_t>(UINT32_MAX);
+  const int64_t group = num_q_heads / num_kv_heads;
+  const PrefillKernel kernel = wide ? prefill_kernel_for<true>(group) : prefill_kernel_for<false>(group);
   int32_t xcd_layout = 0;
   int64_t grid = capacity * num_kv_heads;
   if (num_kv_heads % kXcds == 0) {

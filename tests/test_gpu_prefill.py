@@ -192,6 +192,30 @@ def test_visibility_is_exact(backend, gpu_device, g, bs):
                                        atol=0, err_msg=f"request {i} query {j}")
 
 
+def test_cache_over_4gib(backend, gpu_device):
+    """Caches larger than 4 GiB, whose row byte offsets need more than 32
+    bits: the requests' blocks are moved to the top of each cache."""
+    hkv, g, bs = 8, 2, 256
+    q_lens, k_lens = [70, 5, 130], [300, 700, 130]
+    dev, host = build_case(gpu_device, hkv, g, bs, q_lens, k_lens, seed=41, spare_blocks=0)
+    compact = dev["kc"].shape[0]
+    big = (1 << 32) // (bs * hkv * 128 * 2) + 8  # 4 GiB + 8 blocks per cache
+    shift = big - compact
+    kc = torch.empty((big, bs, hkv, 128), dtype=torch.bfloat16, device=gpu_device)
+    vc = torch.empty_like(kc)
+    try:
+        kc[shift:] = dev["kc"]
+        vc[shift:] = dev["vc"]
+        tables = torch.where(dev["tables"] >= 0, dev["tables"] + shift, dev["tables"])
+        scale = 1.0 / math.sqrt(128)
+        out = backend.paged_attention_prefill(dev["q"], kc, vc, tables, dev["cu_q"], dev["cu_k"],
+                                              scale)
+        check_close(out, *reference(host, scale), "cache over 4 GiB")
+    finally:
+        del kc, vc
+        torch.cuda.empty_cache()
+
+
 def test_unsupported_layouts_raise(backend, gpu_device):
     dev, _ = build_case(gpu_device, 3, 1, 16, [4], [4], seed=1)
     q3 = torch.zeros((4, 9, 128), dtype=torch.bfloat16, device=gpu_device)  # G = 3
