@@ -188,32 +188,38 @@ def main(argv=None) -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    timer = LaunchTimer(stream)
-    store_timer = LaunchTimer(stream)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     start_evt = torch.cuda.Event(enable_timing=True)
     end_evt = torch.cuda.Event(enable_timing=True)
     start_evt.record(stream)
     for _ in range(args.steps):
-        step(timer, store_timer)
+        step()
     end_evt.record(stream)
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
     step_ms = start_evt.elapsed_time(end_evt) / args.steps
     log(f"[bench] {args.steps} steps: {step_ms:.3f} ms/step (wall {wall_s * 1000 / args.steps:.3f})")
+    # Per-kernel breakdown in a pass of its own: the event pairs around each
+    # launch are instrumentation, so they stay out of the timed steps above.
+    timer = LaunchTimer(stream)
+    store_timer = LaunchTimer(stream)
+    for _ in range(args.steps):
+        step(timer, store_timer)
+    torch.cuda.synchronize()
 
     # Same step with the attention consumer instead of the gather.
     for _ in range(args.warmup):
         attention_step()
-    attn_timer = LaunchTimer(stream)
     torch.cuda.synchronize()
     start_evt.record(stream)
     for _ in range(args.steps):
-        attention_step(attn_timer)
+        attention_step()
     end_evt.record(stream)
     torch.cuda.synchronize()
     attn_step_ms = start_evt.elapsed_time(end_evt) / args.steps
+    attn_timer = LaunchTimer(stream)
+    for _ in range(args.steps):
+        attention_step(attn_timer)
     attn_us = attn_timer.durations_us()
     attn_mean = sum(attn_us) / len(attn_us)
     attn_bytes = (total * wl.num_kv_heads * wl.head_dim * 2 * q.element_size()
