@@ -64,6 +64,7 @@ def build_case(device, hkv, g, bs, lens, seed, q_pad_heads=0):
 @pytest.mark.parametrize("hkv,g,bs", [
     (8, 2, 256), (8, 2, 16), (2, 8, 256), (2, 8, 16), (4, 4, 16), (4, 2, 32),
     (8, 1, 16), (2, 1, 16), (1, 8, 16), (1, 1, 4), (2, 4, 8),
+    (8, 2, 24), (2, 4, 1000),  # block sizes that are not powers of two (1000: entries of 500 rows)
 ])
 def test_decode_attention_matches_oracle(backend, gpu_device, hkv, g, bs):
     lens = [0, 1, bs - 1, bs, bs + 1, 3 * bs + 7, 2, 5 * bs, 17, 1]

@@ -85,13 +85,16 @@ def reference(host, scale, tables=None):
 @pytest.mark.parametrize("hkv,g,bs", [
     (8, 2, 256), (8, 2, 16), (2, 8, 16), (4, 4, 32), (1, 1, 16), (2, 4, 8), (8, 1, 256), (1, 8, 64),
     (16, 1, 16), (3, 2, 16), (6, 1, 32),
+    (8, 2, 24), (4, 2, 100),  # block sizes that are not powers of two
 ])
 def test_prefill_matches_oracle(backend, gpu_device, hkv, g, bs):
     """Full prompts (Lq == Lk), continuation chunks over a cached prefix
     (Lk > Lq), single-token chunks, chunks of several query tiles, ragged
-    last blocks, and an empty request.  The kv head counts cover each
-    mapping of workgroups to XCDs: multiples of 8 (8, 16), divisors of 8
-    (1, 2, 4; the plan's length is not a multiple of 8 / H) and neither (3, 6)."""
+    last blocks, and an empty request.  Block sizes of 24 and 100 take the
+    division path of the row map (the others shift).  The kv head counts
+    cover each mapping of workgroups to XCDs: multiples of 8 (8, 16),
+    divisors of 8 (1, 2, 4; the plan's length is not a multiple of 8 / H)
+    and neither (3, 6)."""
     q_lens = [1, 37, 200, 64, 1, 0, 130]
     k_lens = [1, 37, 333, 64 + 3 * bs + 5, 90, 12, 130]
     dev, host = build_case(gpu_device, hkv, g, bs, q_lens, k_lens, seed=hkv * 100 + g * 10 + bs)
