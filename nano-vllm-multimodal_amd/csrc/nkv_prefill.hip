@@ -282,8 +282,8 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
   __shared__ u32x4 k_buf1[kTileChunks];
   __shared__ u32x4 v_buf0[kTileChunks];
   __shared__ u32x4 v_buf1[kTileChunks];
-  __shared__ int32_t rows_buf[3][kPfKeys];  // physical row of each key of a tile, -1 if invalid
-  __shared__ int32_t invalid_buf[3];        // whether a tile has an invalid row
+  __shared__ int32_t rows_buf[4][kPfKeys];  // physical row of each key of a tile, -1 if invalid
+  __shared__ int32_t invalid_buf[4];        // whether a tile has an invalid row
 
   const TileId id = tile_of(blockIdx.x, num_kv_heads, capacity, xcd_layout);
   if (id.entry >= capacity) return;
@@ -346,35 +346,59 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
   const __bf16 one = c16 == 0 ? static_cast<__bf16>(1.f) : static_cast<__bf16>(0.f);
   const bf16x8 ones = {one, one, one, one, one, one, one, one};
 
-  // Rows are resolved two tiles ahead (slots rotate over 3) from block ids
-  // loaded one tile before that; the copies of tile t + 1 are in flight
-  // while tile t is computed.
+  // Software pipeline: tile t computes the softmax and PV of tile t and
+  // the scores of tile t + 1, so the score MFMAs can issue between the
+  // softmax's VALU instructions.  K is copied two tiles ahead (K(t + 2)
+  // into the buffer of K(t), read by the scores of tile t during tile
+  // t - 1), V one tile ahead.  Rows are resolved three tiles ahead, from
+  // block ids loaded one tile before that (slots rotate over 4).
   int32_t ahead_block = -1;  // wavefront 0: block id of its lane's key in the next tile to resolve
   if (wave == 0) {
-    resolve_rows(rows_buf[0], &invalid_buf[0], map, 0, map.block_of(lane), lane);
-    if (num_tiles > 1) {
-      resolve_rows(rows_buf[1], &invalid_buf[1], map, kPfKeys, map.block_of(kPfKeys + lane), lane);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (i < num_tiles) {
+        resolve_rows(rows_buf[i], &invalid_buf[i], map, i * kPfKeys,
+                     map.block_of(i * kPfKeys + lane), lane);
+      }
     }
-    if (num_tiles > 2) ahead_block = map.block_of(2 * kPfKeys + lane);
+    if (num_tiles > 3) ahead_block = map.block_of(3 * kPfKeys + lane);
   }
   __syncthreads();
   issue_copies<kWide, false>(k_buf0, rows_buf[0], k_head, row_bytes, wave, lane);
   issue_copies<kWide, true>(v_buf0, rows_buf[0], v_head, row_bytes, wave, lane);
-  int slot = 0;  // rows slot of the current tile
+  if (num_tiles > 1) issue_copies<kWide, false>(k_buf1, rows_buf[1], k_head, row_bytes, wave, lane);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
   const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses in a V^T read, within 16
   const int tr_dim = 4 * (lane & 3);              // first dim it addresses, within 16
 
+  // S^T = K Q^T over one tile: block (kb, mb) holds keys 16 kb + 4 g4 + i of row m.
+  auto scores = [&](const u32x4* k_tile, f32x4 (&s)[4][2]) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dc = 0; dc < 4; ++dc) {
+        const bf16x8 a = as_bf16x8(k_tile[k_index(16 * kb + c16, 4 * dc + g4)]);
+        s[kb][0] = mfma(a, qb[0][dc], s[kb][0]);
+        s[kb][1] = mfma(a, qb[1][dc], s[kb][1]);
+      }
+    }
+  };
+  f32x4 st[4][2];
+  scores(k_buf0, st);
+
   auto tile_step = [&](auto parity, int32_t tile) {
-    constexpr int kCur = decltype(parity)::value;
-    u32x4* const k_cur = kCur == 0 ? k_buf0 : k_buf1;
+    constexpr int kCur = decltype(parity)::value;  // tile % 2
+    u32x4* const k_this = kCur == 0 ? k_buf0 : k_buf1;  // held K(tile); receives K(tile + 2)
+    u32x4* const k_next = kCur == 0 ? k_buf1 : k_buf0;  // K(tile + 1)
     u32x4* const v_cur = kCur == 0 ? v_buf0 : v_buf1;
-    u32x4* const k_next = kCur == 0 ? k_buf1 : k_buf0;
     u32x4* const v_next = kCur == 0 ? v_buf1 : v_buf0;
     const int32_t key0 = tile * kPfKeys;
-    const int slot1 = slot == 2 ? 0 : slot + 1;
-    const int slot2 = slot1 == 2 ? 0 : slot1 + 1;
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of the tile have landed
-    __syncthreads();                // ... and everyone's; the previous tile is consumed
+    const int slot = tile & 3;
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of K(tile + 1), V(tile) have landed
+    __syncthreads();                // ... and everyone's; tile - 1 is consumed
     const bool has_invalid = invalid_buf[slot] != 0;
     if (has_invalid) {  // zero V of invalid rows (not copied: the buffer holds an older tile)
 #pragma unroll
@@ -384,41 +408,26 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
       }
       __syncthreads();
     }
-    // Wavefront 0 resolves the rows of tile t + 2 from block ids that landed
-    // with the wait above, and loads those of tile t + 3, which land with
-    // the next tile's wait: no wait for the block table on the way.
-    if (wave == 0 && tile + 2 < num_tiles) {
-      resolve_rows(rows_buf[slot2], &invalid_buf[slot2], map, key0 + 2 * kPfKeys, ahead_block,
-                   lane);
-      if (tile + 3 < num_tiles) ahead_block = map.block_of(key0 + 3 * kPfKeys + lane);
+    // The block ids used here landed with the wait above; those loaded
+    // now land with the next tile's.
+    if (wave == 0 && tile + 3 < num_tiles) {
+      const int s3 = (tile + 3) & 3;
+      resolve_rows(rows_buf[s3], &invalid_buf[s3], map, key0 + 3 * kPfKeys, ahead_block, lane);
+      if (tile + 4 < num_tiles) ahead_block = map.block_of(key0 + 4 * kPfKeys + lane);
     }
-    // The copies of tile t + 1 go out in two halves, K before the scores
-    // and V after them, rather than in one burst that every wavefront of
-    // the CU queues on at once.
-    const bool more = tile + 1 < num_tiles;
-    if (more) issue_copies<kWide, false>(k_next, rows_buf[slot1], k_head, row_bytes, wave, lane);
+    if (tile + 2 < num_tiles) {
+      issue_copies<kWide, false>(k_this, rows_buf[(tile + 2) & 3], k_head, row_bytes, wave, lane);
+    }
+    if (tile + 1 < num_tiles) {
+      issue_copies<kWide, true>(v_next, rows_buf[(tile + 1) & 3], v_head, row_bytes, wave, lane);
+    }
     // A tile is plain when every row sees all its keys and all are valid:
     // its scores need no mask.
     const bool plain = !has_invalid && key0 + kPfKeys <= first_row_keys;
 
-    // S^T = K Q^T: block (kb, mb) holds keys 16 kb + 4 g4 + i of row m.
-    f32x4 st[4][2];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      st[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      st[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int dc = 0; dc < 4; ++dc) {
-        const bf16x8 a = as_bf16x8(k_cur[k_index(16 * kb + c16, 4 * dc + g4)]);
-        st[kb][0] = mfma(a, qb[0][dc], st[kb][0]);
-        st[kb][1] = mfma(a, qb[1][dc], st[kb][1]);
-      }
-    }
-    if (more) issue_copies<kWide, true>(v_next, rows_buf[slot1], v_head, row_bytes, wave, lane);
-
-    // Online softmax per row (exp2 units); P^T operands for both 32-key steps.
-    bf16x8 pb[2][2];
+    // Online softmax per row (exp2 units): mask, max and the rare rescale.
     const int4* rows_now = reinterpret_cast<const int4*>(rows_buf[slot]);
+    float ref[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       if (!plain) {  // hide keys past the row's limit or in invalid rows
@@ -451,25 +460,37 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
       }
       // A row with nothing visible yet keeps the reference -inf: its
       // weights are 0 (hidden scores are -inf too).
-      const float ref = row_max[mb] == -INFINITY ? INFINITY : row_max[mb];
-      float p[4][4];
+      ref[mb] = row_max[mb] == -INFINITY ? INFINITY : row_max[mb];
+    }
+
+    // Weights of this tile, then the scores of the next tile.  After the
+    // last tile the scores read a stale buffer and are dropped.
+    bf16x8 pb[2][2];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][mb][i], scale_log2, -ref));
-        }
+    for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         bf16x8 w;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          w[i] = static_cast<__bf16>(p[2 * c][i]);
-          w[4 + i] = static_cast<__bf16>(p[2 * c + 1][i]);
+          w[i] = static_cast<__bf16>(
+              __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * c][mb][i], scale_log2, -ref[mb])));
+          w[4 + i] = static_cast<__bf16>(
+              __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * c + 1][mb][i], scale_log2, -ref[mb])));
         }
         pb[c][mb] = w;
       }
     }
+    scores(k_next, st);
+    // Scheduler order for the scores: four K operand reads ahead, then
+    // each read's two MFMAs with the next read.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the PV product is scheduled on its own
 
     // O^T += V^T P^T.  Step c covers keys 32 c .. +32 in the order the P^T
     // operand holds them: slots 0-3 = keys 32c + 4 g4 + j, slots 4-7 = keys
@@ -490,7 +511,6 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
       acc[8][0] = mfma(ones, pb[c][0], acc[8][0]);
       acc[8][1] = mfma(ones, pb[c][1], acc[8][1]);
     }
-    slot = slot1;
   };
   for (int32_t tile = 0; tile < num_tiles; tile += 2) {
     tile_step(std::integral_constant<int, 0>{}, tile);
