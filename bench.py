@@ -98,7 +98,8 @@ def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(the paged-KV store/gather path is rank-local; see DESIGN.md for sharding)",
+              "(the paged-KV store/gather path is rank-local: under tensor parallelism each rank "
+              "runs it on its own kv heads with the same slot_mapping and block tables)",
               file=sys.stderr)
         return 2
 

@@ -72,7 +72,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // the one being copied into and does not wait for the copies in flight.
 constexpr int kTileChunks = kPfKeys * 16;  // 16-byte chunks per K or V tile
 
-__device__ __forceinline__ int k_index(int key, int chunk) { return key * 16 + (chunk ^ (key & 15)); }
+__device__ __forceinline__ int k_index(int key, int chunk) {
+  return key * 16 + (chunk ^ (key & 15));
+}
 __device__ __forceinline__ int v_index(int key, int chunk) {
   return key * 16 + (chunk ^ ((key & 7) << 1));
 }
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
   if (num_tiles > 1) issue_copies<kWide, false>(k_buf1, rows_buf[1], k_head, row_bytes, wave, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses in a V^T read, within 16
+  const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses in a V^T read (of 16)
   const int tr_dim = 4 * (lane & 3);              // first dim it addresses, within 16
 
   // S^T = K Q^T over one tile: block (kb, mb) holds keys 16 kb + 4 g4 + i of row m.
@@ -657,7 +659,8 @@ extern "C" int nkv_paged_attention_prefill(
   const int64_t row_bytes = num_kv_heads * head_dim * 2;
   const bool wide = num_blocks * block_size * row_bytes > static_cast<int64_t>(UINT32_MAX);
   const int64_t group = num_q_heads / num_kv_heads;
-  const PrefillKernel kernel = wide ? prefill_kernel_for<true>(group) : prefill_kernel_for<false>(group);
+  const PrefillKernel kernel =
+      wide ? prefill_kernel_for<true>(group) : prefill_kernel_for<false>(group);
   int32_t xcd_layout = 0;
   int64_t grid = capacity * num_kv_heads;
   if (num_kv_heads % kXcds == 0) {
