@@ -220,6 +220,13 @@ class HIPPagedKVBackend:
         self._load()
         if plan is None:
             plan = self.build_attention_plan(key_cache, cu_seqlens_k, total_tokens)
+        else:
+            need = int(_lib.load_library().nkv_attention_plan_capacity(
+                total_tokens, block_tables.shape[0], key_cache.shape[1]))
+            if plan[0].shape[0] < need:
+                raise ValueError(f"attention plan has {plan[0].shape[0]} entries, {total_tokens} "
+                                 f"context rows need {need}: build it with build_attention_plan "
+                                 "for the same lengths and block size")
         if out is None:
             out = torch.empty_like(q)
         ops.paged_attention_decode(

@@ -346,7 +346,17 @@ def _paged_attention_prefill_impl(q, key_cache, value_cache, block_tables, cu_se
         raise ValueError("q head_dim does not match the cache")
     if plan.dtype != torch.int32 or plan.ndim != 2 or plan.shape[1] != 4 or not plan.is_contiguous():
         raise ValueError("prefill plan must be a contiguous [capacity, 4] int32 tensor")
-    status = _lib.load_library().nkv_paged_attention_prefill(
+    library = _lib.load_library()
+    if num_kv_heads > 0 and q.shape[1] % num_kv_heads == 0:
+        # A plan built for these queries and this head layout has at least
+        # this many entries; one built for a layout with longer query tiles
+        # has fewer (its tiles would not fit this kernel's).
+        need = int(library.nkv_prefill_plan_capacity(q.shape[0], num_seqs,
+                                                     q.shape[1] // num_kv_heads))
+        if plan.shape[0] < need:
+            raise ValueError(f"prefill plan has {plan.shape[0]} entries, these queries need {need}: "
+                             "build it with build_prefill_plan for the same q and cu_seqlens_q")
+    status = library.nkv_paged_attention_prefill(
         q.data_ptr(), q.stride(0), key_cache.data_ptr(), value_cache.data_ptr(),
         block_tables.data_ptr(), block_tables.shape[1], cu_seqlens_q.data_ptr(),
         cu_seqlens_k.data_ptr(), plan.data_ptr() if plan.shape[0] else None, plan.shape[0],

@@ -93,6 +93,18 @@ def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):
         check_close(out, ref, "planned")
 
 
+def test_plan_for_other_lengths_is_rejected(backend, gpu_device):
+    """A plan sized for shorter contexts cannot cover these: refused on the
+    host instead of leaving rows out."""
+    lens = [300, 1, 513, 256, 40]
+    dev, _, total = build_case(gpu_device, 8, 2, 16, lens, seed=9)
+    short = torch.tensor([0, 1, 2, 3, 4, 5], dtype=torch.int32, device=gpu_device)
+    plan = backend.build_attention_plan(dev["kc"], short, 5)
+    with pytest.raises(ValueError, match="attention plan"):
+        backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev["tables"], dev["cu"],
+                                       total, 0.1, plan=plan)
+
+
 @pytest.mark.parametrize("hkv,g,bs", [(8, 2, 16), (2, 4, 8), (4, 2, 4), (1, 1, 1024)])
 def test_long_contexts_over_small_blocks(backend, gpu_device, hkv, g, bs):
     """Entries span many blocks (512 rows of 8- or 16-row blocks, 256 rows =

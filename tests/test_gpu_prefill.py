@@ -227,6 +227,18 @@ def test_unsupported_layouts_raise(backend, gpu_device):
                                         dev["cu_k"], 0.1)
 
 
+def test_plan_for_another_head_layout_is_rejected(backend, gpu_device):
+    """A plan built for one query head per kv head has 128-token tiles; the
+    two-heads-per-kv-head kernel takes 64-token tiles, so reusing it would
+    leave queries out.  Its size gives it away."""
+    q_lens, k_lens = [300, 40], [300, 90]
+    dev, _ = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=13)
+    q1 = dev["q"][:, :8]  # one query head per kv head
+    plan1 = backend.build_prefill_plan(q1, dev["kc"], dev["cu_q"])
+    with pytest.raises(ValueError, match="prefill plan"):
+        run(backend, dev, 0.1, plan=plan1)
+
+
 def test_chunked_prefill_full_size(backend, gpu_device):
     """The chunked-prefill step at full size: 16 requests in one 8192-token
     chunk (lengths uniform in [128, 4096] scaled to the chunk), requests 0-7
