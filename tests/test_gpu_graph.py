@@ -7,7 +7,8 @@ slot -1 and context length 0 past the batch, block_tables[:bs, :w]
 rewritten, stale columns and rows kept.  A graph of plan + per-layer store
 + planned varlen gather is captured once and replayed for several batches,
 with eager packing between replays, every replay checked against the
-oracle (no memset is recorded in the graph).
+oracle (no memset is recorded in the graph).  So is the Flash path's graph
+decode: per-layer store + the flash_attn_with_kvcache drop-in.
 """
 from __future__ import annotations
 
@@ -124,3 +125,78 @@ def test_captured_decode_graph_replays_match_oracle(gpu_device):
             v_out[:total].cpu().view(torch.int16).numpy(),
             oracle.gather_varlen(host[1, last], exp["block_tables"], n), err_msg=f"replay {replay} V")
     del plan_keepalive
+
+
+def test_captured_flash_decode_replays_match_oracle(gpu_device):
+    """The reference's graph decode on the Flash path (model_runner.py:
+    1079-1157 captures Attention.forward; attention.py:87-93 store,
+    :122-130 flash_attn_with_kvcache), with the drop-in from nanokv.flash:
+    per layer, store then decode attention over the paged cache, captured
+    once and replayed for batches of 1..bucket sequences (padding rows have
+    context length 0).  Every replay's cache is checked bit for bit and its
+    attention output within 1e-3 + 1e-2 |ref| (fp32 accumulation, one bf16
+    rounding) against the oracle."""
+    from nanokv.flash import flash_attn_with_kvcache
+    from nanokv.packing import DecodeGraphBuffers, DevicePacker, SequenceBatch
+    from nanokv.paged_kv import create_paged_kv_backend
+
+    backend = create_paged_kv_backend("hip")
+    rng = np.random.default_rng(3)
+    layers, bucket, max_blocks, num_blocks, kv_heads, q_heads, dim = 2, 8, 6, 64, 8, 16, 128
+    scale = 1.0 / np.sqrt(dim)
+    shape = (2, layers, num_blocks, BS, kv_heads, dim)
+    cache = torch.randn(shape, dtype=torch.float32, device=gpu_device).to(torch.bfloat16)
+    buffers = DecodeGraphBuffers.allocate(gpu_device, max_num_seqs=bucket, max_blocks=max_blocks)
+    packer = DevicePacker(gpu_device, BS)
+    key_in = torch.zeros((layers, bucket, kv_heads, dim), dtype=torch.bfloat16, device=gpu_device)
+    value_in = torch.zeros_like(key_in)
+    q_in = torch.zeros((bucket, q_heads, dim), dtype=torch.bfloat16, device=gpu_device)
+
+    n, tables = random_batch(rng, bucket, max_blocks * BS, num_blocks)
+    packer.pack_decode_into(SequenceBatch.from_block_lists(n, tables), buffers)
+
+    def decode_work():
+        outs = []
+        for layer in range(layers):
+            kc, vc = cache[0, layer], cache[1, layer]
+            backend.store(key_in[layer], value_in[layer], kc, vc, buffers.slot_mapping)
+            outs.append(flash_attn_with_kvcache(q_in.unsqueeze(1), kc, vc,
+                                                cache_seqlens=buffers.context_lens,
+                                                block_table=buffers.block_tables,
+                                                softmax_scale=scale, causal=True))
+        return outs
+
+    decode_work()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = decode_work()
+    torch.cuda.synchronize()
+
+    host = cache.cpu().view(torch.int16).numpy().copy()
+    for replay in range(4):
+        num_seqs = int(rng.integers(1, bucket + 1))
+        n, tables = random_batch(rng, num_seqs, max_blocks * BS, num_blocks)
+        ctx = packer.pack_decode_into(SequenceBatch.from_block_lists(n, tables), buffers)
+        key_in.copy_(torch.randn(key_in.shape, device=gpu_device).to(torch.bfloat16))
+        value_in.copy_(torch.randn(value_in.shape, device=gpu_device).to(torch.bfloat16))
+        q_in.copy_(torch.randn(q_in.shape, device=gpu_device).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        slots = ctx.slot_mapping.cpu().numpy()
+        padded_slots = np.concatenate([slots, np.full(bucket - num_seqs, -1, np.int32)])
+        seqs = [oracle.SeqState(int(n[i]), tables[i]) for i in range(num_seqs)]
+        exp = oracle.prepare_decode(seqs, BS)
+        q_host = q_in[:num_seqs].float().cpu().numpy()
+        for layer in range(layers):
+            hk, hv = host[0, layer], host[1, layer]
+            oracle.store(key_in[layer].cpu().view(torch.int16).numpy(),
+                         value_in[layer].cpu().view(torch.int16).numpy(), hk, hv, padded_slots)
+            ref = oracle.paged_attention_decode(q_host, hk, hv, exp["block_tables"], n, scale)
+            got = outs[layer][:, 0].float().cpu().numpy()
+            bad = np.abs(got[:num_seqs] - ref) > 1e-3 + 1e-2 * np.abs(ref)
+            assert not bad.any(), f"replay {replay} layer {layer}: {int(bad.sum())} elements off"
+            assert not got[num_seqs:].any(), f"replay {replay} layer {layer}: padding rows not zero"
+        np.testing.assert_array_equal(cache.cpu().view(torch.int16).numpy(), host,
+                                      err_msg=f"replay {replay}")
