@@ -433,7 +433,7 @@ def measure_prefill_attention(device, backend, reps: int) -> dict:
     cu_k = torch.tensor(np.concatenate([[0], np.cumsum(k_lens)]), dtype=torch.int32, device=device)
     q = torch.randn((sum(q_lens), hkv * g, dim), device=device, generator=gen).to(torch.bfloat16)
     scale = 1.0 / math.sqrt(dim)
-    plan = backend.build_prefill_plan(q, kc, cu_q)
+    plan = backend.build_prefill_plan(q, kc, cu_q, cu_k)
     out = torch.empty_like(q)
     stream = torch.cuda.current_stream(device)
     timer = LaunchTimer(stream)

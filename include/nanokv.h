@@ -300,8 +300,11 @@ int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
  * nkv_build_prefill_plan cuts every request's queries into tiles of
  *   nkv_prefill_tile_tokens(G) tokens (128 / G) and writes one int4
  *   {seq, token0, tokens, 0} per tile into `plan` (capacity >=
- *   nkv_prefill_plan_capacity(total query tokens, num_seqs, G)).  It reads
- *   only cu_seqlens_q, so one plan serves every layer of a step.
+ *   nkv_prefill_plan_capacity(total query tokens, num_seqs, G)).  Tiles
+ *   are listed by the number of keys they see, most first (plans of up to
+ *   2048 entries; longer ones request by request, last tile first).  It
+ *   reads only cu_seqlens_q and cu_seqlens_k, so one plan serves every
+ *   layer of a step.
  * nkv_paged_attention_prefill runs one workgroup per (tile, kv head);
  *   block_tables [num_seqs, table_stride] (int32, -1 padded); a block id
  *   outside [0, num_blocks) or a row past the table drops its keys.  q and
@@ -312,7 +315,8 @@ int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
 int64_t nkv_prefill_tile_tokens(int64_t group);
 int64_t nkv_prefill_plan_capacity(int64_t total_q_tokens, int64_t num_seqs,
                                   int64_t group);
-int nkv_build_prefill_plan(const int32_t* cu_seqlens_q, int64_t num_seqs,
+int nkv_build_prefill_plan(const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqlens_k, int64_t num_seqs,
                            int64_t group, void* plan, int64_t capacity,
                            void* stream);
 int nkv_paged_attention_prefill(const void* q, int64_t q_token_stride,

@@ -101,13 +101,22 @@ __device__ __forceinline__ float row4_sum(float x) {
 }
 
 // Plan: one int4 {seq, token0, tokens, 0} per workgroup: tokens [token0,
-// token0 + tokens) of sequence seq's queries, tokens <= tile_tokens.  A
-// sequence's tiles are listed last tile first: later queries see more keys,
-// so the longest workgroups are dispatched first and the short ones fill
-// the tail.  Entries past the total get tokens = 0.
+// token0 + tokens) of sequence seq's queries, tokens <= tile_tokens.
+// Entries past the total get tokens = 0.  The tiles are listed longest
+// first (most visible keys: the keys of a tile's last query), so that the
+// longest workgroups start first and the short ones fill the tail; ties in
+// plan order.  Plans of up to kPfSortMax tiles are sorted in LDS by one
+// workgroup (bitonic); longer ones list each sequence's tiles last tile
+// first, sequence after sequence.
+#ifndef NKV_PF_SORT_MAX
+#define NKV_PF_SORT_MAX 2048  // longest plan sorted in LDS (0: never sort)
+#endif
+constexpr int kPfSortMax = NKV_PF_SORT_MAX;
+
 __global__ __launch_bounds__(kPfPlanThreads) void prefill_plan_kernel(
-    const int32_t* __restrict__ cu_seqlens_q, int32_t num_seqs, int32_t tile_tokens,
-    int4* __restrict__ plan, int64_t capacity) {
+    const int32_t* __restrict__ cu_seqlens_q, const int32_t* __restrict__ cu_seqlens_k,
+    int32_t num_seqs, int32_t tile_tokens, int4* __restrict__ plan, int64_t capacity,
+    int32_t sort) {
   extern __shared__ int32_t s_mem[];
   int32_t* s_first = s_mem;               // [num_seqs + 1]
   int32_t* s_tmp = s_mem + num_seqs + 1;  // [kPfPlanThreads / 64 + 1]
@@ -119,18 +128,57 @@ __global__ __launch_bounds__(kPfPlanThreads) void prefill_plan_kernel(
       },
       s_first, s_tmp);
   const int64_t total = s_first[num_seqs];
+  // Entry e in sequence order: sequence i's tiles, last tile first.
+  auto entry_of = [&](int32_t e) {
+    const int32_t i = owner_of(s_first, num_seqs, e);
+    const int32_t tiles = s_first[i + 1] - s_first[i];
+    const int32_t t0 = (tiles - 1 - (e - s_first[i])) * tile_tokens;
+    const int32_t len = cu_seqlens_q[i + 1] - cu_seqlens_q[i];
+    return make_int4(i, t0, min(tile_tokens, len - t0), 0);
+  };
+  if (sort && total <= kPfSortMax) {  // one workgroup (the launch makes sure)
+    // Sort keys: (2^31 - 1 - visible keys) << 32 | e, ascending; padding last.
+    const int32_t key_offset = (num_seqs + kPfPlanThreads / 64 + 3) & ~1;  // 8-byte aligned
+    uint64_t* s_key = reinterpret_cast<uint64_t*>(s_mem + key_offset);
+    int32_t n2 = 1;
+    while (n2 < total) n2 <<= 1;
+    for (int32_t e = threadIdx.x; e < n2; e += kPfPlanThreads) {
+      uint64_t key = ~uint64_t{0};
+      if (e < total) {
+        const int4 en = entry_of(e);
+        const int32_t lq = cu_seqlens_q[en.x + 1] - cu_seqlens_q[en.x];
+        const int32_t lk = cu_seqlens_k[en.x + 1] - cu_seqlens_k[en.x];
+        const int32_t visible = max(0, lk - lq + en.y + en.z);
+        key = (static_cast<uint64_t>(0x7FFFFFFF - visible) << 32) | static_cast<uint32_t>(e);
+      }
+      s_key[e] = key;
+    }
+    for (int32_t k = 2; k <= n2; k <<= 1) {
+      for (int32_t j = k >> 1; j > 0; j >>= 1) {
+        __syncthreads();
+        for (int32_t i = threadIdx.x; i < n2; i += kPfPlanThreads) {
+          const int32_t partner = i ^ j;
+          if (partner > i) {
+            const uint64_t a = s_key[i], b = s_key[partner];
+            if ((a > b) == ((i & k) == 0)) {
+              s_key[i] = b;
+              s_key[partner] = a;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < capacity; e += kPfPlanThreads) {
+      plan[e] = e < total ? entry_of(static_cast<int32_t>(s_key[e] & 0xFFFFFFFFu))
+                          : make_int4(0, 0, 0, 0);
+    }
+    return;
+  }
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kPfPlanThreads;
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * kPfPlanThreads + threadIdx.x; e < capacity;
        e += stride) {
-    int4 entry = make_int4(0, 0, 0, 0);
-    if (e < total) {
-      const int32_t i = owner_of(s_first, num_seqs, static_cast<int32_t>(e));
-      const int32_t tiles = s_first[i + 1] - s_first[i];
-      const int32_t t0 = (tiles - 1 - (static_cast<int32_t>(e) - s_first[i])) * tile_tokens;
-      const int32_t len = cu_seqlens_q[i + 1] - cu_seqlens_q[i];
-      entry = make_int4(i, t0, min(tile_tokens, len - t0), 0);
-    }
-    plan[e] = entry;
+    plan[e] = e < total ? entry_of(static_cast<int32_t>(e)) : make_int4(0, 0, 0, 0);
   }
 }
 
@@ -569,8 +617,9 @@ extern "C" int64_t nkv_prefill_plan_capacity(int64_t total_q_tokens, int64_t num
   return (total_q_tokens + tile - 1) / tile + num_seqs;
 }
 
-extern "C" int nkv_build_prefill_plan(const int32_t* cu_seqlens_q, int64_t num_seqs,
-                                      int64_t group, void* plan, int64_t capacity, void* stream) {
+extern "C" int nkv_build_prefill_plan(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                      int64_t num_seqs, int64_t group, void* plan,
+                                      int64_t capacity, void* stream) {
   using namespace nkv;
   const int64_t tile = nkv_prefill_tile_tokens(group);
   if (tile == 0) {
@@ -583,19 +632,24 @@ extern "C" int nkv_build_prefill_plan(const int32_t* cu_seqlens_q, int64_t num_s
                     static_cast<long long>(capacity));
   }
   if (capacity == 0) return NKV_OK;
-  if (!plan || (num_seqs > 0 && !cu_seqlens_q)) {
+  if (!plan || (num_seqs > 0 && (!cu_seqlens_q || !cu_seqlens_k))) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: null pointer");
   }
   if (reinterpret_cast<uint64_t>(plan) % 16 != 0) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: plan must be 16-byte aligned");
   }
-  const int64_t blocks = (capacity + kPfPlanThreads - 1) / kPfPlanThreads;
-  const size_t lds = (static_cast<size_t>(num_seqs) + 1 + kPfPlanThreads / kWave + 1) *
-                     sizeof(int32_t);
+  // Plans that fit the LDS sort are built by one workgroup, longest tile
+  // first; longer ones by a grid, in sequence order.
+  const bool sort = capacity <= kPfSortMax;
+  const int64_t blocks = sort ? 1 : (capacity + kPfPlanThreads - 1) / kPfPlanThreads;
+  const size_t scan_ints = static_cast<size_t>(num_seqs) + 1 + kPfPlanThreads / kWave + 1;
+  const size_t lds = sort ? ((scan_ints + 1) & ~size_t{1}) * sizeof(int32_t) +
+                                kPfSortMax * sizeof(uint64_t)
+                          : scan_ints * sizeof(int32_t);
   prefill_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kPfPlanThreads), lds,
                         static_cast<hipStream_t>(stream)>>>(
-      cu_seqlens_q, static_cast<int32_t>(num_seqs), static_cast<int32_t>(tile),
-      static_cast<int4*>(plan), capacity);
+      cu_seqlens_q, cu_seqlens_k, static_cast<int32_t>(num_seqs), static_cast<int32_t>(tile),
+      static_cast<int4*>(plan), capacity, sort ? 1 : 0);
   return nkv_check_launch("nkv_build_prefill_plan");
 }
 

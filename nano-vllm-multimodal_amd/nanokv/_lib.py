@@ -92,7 +92,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "nkv_prefill_tile_tokens": (c_i64, (c_i64,)),
     "nkv_prefill_plan_capacity": (c_i64, (c_i64, c_i64, c_i64)),
-    "nkv_build_prefill_plan": (ctypes.c_int, (c_ptr, c_i64, c_i64, c_ptr, c_i64, c_ptr)),
+    "nkv_build_prefill_plan": (ctypes.c_int, (c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_i64, c_ptr)),
     "nkv_paged_attention_prefill": (
         ctypes.c_int,
         (

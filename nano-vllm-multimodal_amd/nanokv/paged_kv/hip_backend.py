@@ -235,13 +235,13 @@ class HIPPagedKVBackend:
         return out
 
     def build_prefill_plan(self, q: torch.Tensor, key_cache: torch.Tensor,
-                           cu_seqlens_q: torch.Tensor) -> torch.Tensor:
-        """Query tiles for :meth:`paged_attention_prefill`; depends on
-        cu_seqlens_q and the head layout only, so one plan serves every layer
-        of a step."""
+                           cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor) -> torch.Tensor:
+        """Query tiles for :meth:`paged_attention_prefill`, the tiles that see
+        the most keys first; depends on the lengths and the head layout
+        only, so one plan serves every layer of a step."""
         self._load()
         group = q.shape[1] // key_cache.shape[2]
-        return ops.build_prefill_plan(cu_seqlens_q, q.shape[0], group)
+        return ops.build_prefill_plan(cu_seqlens_q, cu_seqlens_k, q.shape[0], group)
 
     def paged_attention_prefill(
         self,
@@ -279,7 +279,7 @@ class HIPPagedKVBackend:
             raise ValueError("q must be [tokens, num_q_heads, head_dim] on the caches' device")
         self._load()
         if plan is None:
-            plan = self.build_prefill_plan(q, key_cache, cu_seqlens_q)
+            plan = self.build_prefill_plan(q, key_cache, cu_seqlens_q, cu_seqlens_k)
         if out is None:
             out = torch.empty_like(q)
         ops.paged_attention_prefill(q, key_cache, value_cache, block_tables, cu_seqlens_q,

@@ -56,8 +56,8 @@ SCHEMAS = {
     "paged_attention_decode": "paged_attention_decode(Tensor q, Tensor key_cache, "
     "Tensor value_cache, Tensor block_tables, Tensor plan, Tensor first_part, float scale, "
     "Tensor(a!) out) -> ()",
-    "build_prefill_plan": "build_prefill_plan(Tensor cu_seqlens_q, int total_q_tokens, "
-    "int group) -> Tensor",
+    "build_prefill_plan": "build_prefill_plan(Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
+    "int total_q_tokens, int group) -> Tensor",
     "paged_attention_prefill": "paged_attention_prefill(Tensor q, Tensor key_cache, "
     "Tensor value_cache, Tensor block_tables, Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
     "Tensor plan, float scale, Tensor(a!) out) -> ()",
@@ -309,17 +309,18 @@ def _require_cu(name: str, cu: torch.Tensor, num_seqs: int | None = None) -> int
     return cu.numel() - 1
 
 
-def _build_prefill_plan_impl(cu_seqlens_q, total_q_tokens: int, group: int):
-    device = _require_device("paged KV HIP prefill plan", cu_seqlens_q)
+def _build_prefill_plan_impl(cu_seqlens_q, cu_seqlens_k, total_q_tokens: int, group: int):
+    device = _require_device("paged KV HIP prefill plan", cu_seqlens_q, cu_seqlens_k)
     num_seqs = _require_cu("cu_seqlens_q", cu_seqlens_q)
+    _require_cu("cu_seqlens_k", cu_seqlens_k, num_seqs)
     library = _lib.load_library()
     capacity = int(library.nkv_prefill_plan_capacity(total_q_tokens, num_seqs, group))
     if capacity == 0 and total_q_tokens > 0:
         raise ValueError("prefill attention supports 1, 2, 4 or 8 query heads per kv head")
     plan = torch.empty((capacity, 4), dtype=torch.int32, device=device)
     status = library.nkv_build_prefill_plan(
-        cu_seqlens_q.data_ptr(), num_seqs, group, plan.data_ptr() if capacity else None, capacity,
-        _stream(device),
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_seqs, group,
+        plan.data_ptr() if capacity else None, capacity, _stream(device),
     )
     _lib.check(status, "nanovllm_paged_kv::build_prefill_plan")
     return plan
@@ -355,7 +356,7 @@ def _paged_attention_prefill_impl(q, key_cache, value_cache, block_tables, cu_se
                                                      q.shape[1] // num_kv_heads))
         if plan.shape[0] < need:
             raise ValueError(f"prefill plan has {plan.shape[0]} entries, these queries need {need}: "
-                             "build it with build_prefill_plan for the same q and cu_seqlens_q")
+                             "build it with build_prefill_plan for the same q and cu_seqlens")
     status = library.nkv_paged_attention_prefill(
         q.data_ptr(), q.stride(0), key_cache.data_ptr(), value_cache.data_ptr(),
         block_tables.data_ptr(), block_tables.shape[1], cu_seqlens_q.data_ptr(),

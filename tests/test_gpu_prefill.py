@@ -103,6 +103,29 @@ def test_prefill_matches_oracle(backend, gpu_device, hkv, g, bs):
     check_close(out, *reference(host, scale), f"hkv={hkv} g={g} bs={bs}")
 
 
+def check_plan(plan, q_lens, k_lens, tile, longest_first):
+    """Every query tile exactly once, entries past the tiles empty, and the
+    order: most visible keys first (ties in sequence order, each sequence's
+    last tile first), or, for plans too long to sort, sequence by sequence,
+    last tile first."""
+    total = sum(-(-n // tile) for n in q_lens)
+    entries = plan[:total]
+    got = sorted((int(s), int(t0), int(n)) for s, t0, n, _ in entries)
+    want = sorted((i, t0, min(tile, n - t0)) for i, n in enumerate(q_lens) for t0 in range(0, n, tile))
+    assert got == want
+    assert not plan[total:, 2].any()
+    order = [(int(s), int(t0)) for s, t0, _, _ in entries]
+    by_sequence = [(i, t0) for i, n in enumerate(q_lens) for t0 in reversed(range(0, n, tile))]
+    if longest_first:
+        visible = [k_lens[s] - q_lens[s] + t0 + int(n) for s, t0, n, _ in entries]
+        rank = {key: r for r, key in enumerate(by_sequence)}
+        assert order == sorted(order, key=lambda k: (-(k_lens[k[0]] - q_lens[k[0]] + k[1]
+                                                       + min(tile, q_lens[k[0]] - k[1])), rank[k]))
+        assert visible == sorted(visible, reverse=True)
+    else:
+        assert order == by_sequence
+
+
 def test_plan_tiles_cover_every_query(backend, gpu_device):
     from nanokv import _lib
 
@@ -110,14 +133,29 @@ def test_plan_tiles_cover_every_query(backend, gpu_device):
     dev, host = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=3)
     tile = int(_lib.load_library().nkv_prefill_tile_tokens(2))
     assert tile in (64, 128)  # 128 or 256 query rows per workgroup, 2 heads per token
-    plan = backend.build_prefill_plan(dev["q"], dev["kc"], dev["cu_q"]).cpu().numpy()
-    expect = [-(-n // tile) for n in q_lens]
-    entries = plan[: sum(expect)]
-    for i, n in enumerate(q_lens):
-        own = entries[entries[:, 0] == i]
-        assert own[:, 1].tolist() == list(range(0, n, tile))[::-1]  # last tile first
-        assert int(own[:, 2].sum()) == n
-    assert not plan[sum(expect):, 2].any()
+    plan = backend.build_prefill_plan(dev["q"], dev["kc"], dev["cu_q"], dev["cu_k"]).cpu().numpy()
+    check_plan(plan, q_lens, k_lens, tile, longest_first=True)
+
+
+@pytest.mark.parametrize("num_seqs,mean_tokens", [(37, 300), (700, 900)])
+def test_plan_order_at_scale(gpu_device, num_seqs, mean_tokens):
+    """Random lengths and cached prefixes: 37 requests (a plan whose length
+    is not a power of two, sorted in LDS) and 700 requests at 8 query heads
+    per kv head (over 2048 tiles: the unsorted fallback)."""
+    from nanokv import _lib
+    from nanokv.paged_kv import ops
+
+    rng = np.random.default_rng(num_seqs)
+    q_lens = rng.integers(0, 2 * mean_tokens, num_seqs).tolist()
+    k_lens = [q + int(c) for q, c in zip(q_lens, rng.integers(0, 3000, num_seqs))]
+    group = 2 if num_seqs < 100 else 8
+    tile = int(_lib.load_library().nkv_prefill_tile_tokens(group))
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32, device=gpu_device)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(k_lens)]), dtype=torch.int32, device=gpu_device)
+    plan = ops.build_prefill_plan(cu_q, cu_k, sum(q_lens), group).cpu().numpy()
+    tiles = sum(-(-n // tile) for n in q_lens)
+    assert (tiles <= 2048) == (num_seqs < 100)
+    check_plan(plan, q_lens, k_lens, tile, longest_first=plan.shape[0] <= 2048)
 
 
 def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):
@@ -126,7 +164,7 @@ def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):
     q_lens, k_lens = [70, 9], [100, 9]
     dev, host = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=7, q_extra_heads=8)
     assert dev["q"].stride(0) == 24 * 128
-    plan = backend.build_prefill_plan(dev["q"], dev["kc"], dev["cu_q"])
+    plan = backend.build_prefill_plan(dev["q"], dev["kc"], dev["cu_q"], dev["cu_k"])
     out = torch.empty((sum(q_lens), 16, 128), dtype=torch.bfloat16, device=gpu_device)
     ref, ref_abs = reference(host, 0.1)
     for _ in range(2):
@@ -234,7 +272,7 @@ def test_plan_for_another_head_layout_is_rejected(backend, gpu_device):
     q_lens, k_lens = [300, 40], [300, 90]
     dev, _ = build_case(gpu_device, 8, 2, 16, q_lens, k_lens, seed=13)
     q1 = dev["q"][:, :8]  # one query head per kv head
-    plan1 = backend.build_prefill_plan(q1, dev["kc"], dev["cu_q"])
+    plan1 = backend.build_prefill_plan(q1, dev["kc"], dev["cu_q"], dev["cu_k"])
     with pytest.raises(ValueError, match="prefill plan"):
         run(backend, dev, 0.1, plan=plan1)
 
