@@ -239,7 +239,8 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  * straight from the paged caches, with no gather.
  *   out[i, h, :] = softmax(scale * q[i, h] . K_i[:, h / G]^T) V_i[:, h / G]
  * for query head h, G = num_q_heads / num_kv_heads (kv head h / G), in fp32
- * with a bf16 result.  An empty context yields zeros.  bf16 only,
+ * with a result in the input type.  An empty context yields zeros.  dtype
+ * NKV_DTYPE_BFLOAT16 or NKV_DTYPE_FLOAT16 (q, caches and out alike),
  * head_dim 128, num_kv_heads in {1,2,4,8}, at most 16 query heads.
  *
  * Replaces: the decode call flash_attn_with_kvcache(q, k_cache, v_cache,
@@ -286,7 +287,8 @@ int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
 /*
  * Paged-attention prefill: causal attention of each sequence's chunk of
  * query tokens over its context, read straight from the paged cache
- * (head_dim 128, bfloat16, query heads per kv head G = 1, 2, 4 or 8).
+ * (head_dim 128, bfloat16 or float16 for q, caches and out alike, query
+ * heads per kv head G = 1, 2, 4 or 8).
  * Request i has query rows [cu_seqlens_q[i], cu_seqlens_q[i+1]) (Lq) and
  * context rows [0, Lk), Lk = cu_seqlens_k[i+1] - cu_seqlens_k[i] >= Lq;
  * query j sees keys [0, Lk - Lq + j]; query head h reads kv head h / G.

@@ -13,7 +13,7 @@
 // query head (reference max m, weight sum l, unnormalised output), and a
 // reduce kernel merges the partials of each (sequence, query head).
 //
-// Mapping inside a workgroup (8 waves, head_dim 128, bf16):
+// Mapping inside a workgroup (8 waves, head_dim 128, bf16 or fp16):
 //   * the entry's cache rows are resolved once through the block table into
 //     LDS (invalid block ids give rows that are skipped);
 //   * a 16-lane DPP row owns one (row, kv head): each lane holds 8 dims
@@ -21,7 +21,7 @@
 //     cache bytes (coalesced, non-temporal); the waves take interleaved
 //     groups of rows, so the workgroup sweeps its rows as one front;
 //   * q.k for the G = Hq/Hkv query heads of that kv head is 4 v_dot2 on
-//     packed bf16 pairs plus a 4-step DPP row sum (fp32);
+//     packed bf16 / fp16 pairs plus a 4-step DPP row sum (fp32);
 //   * an online softmax in fp32 with exp2 (scale * log2 e folded in);
 //   * the waves merge in LDS without a barrier: the last one to arrive
 //     stores the entry's partials (fp16 sums with a power-of-two scale).
@@ -105,12 +105,27 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                          __builtin_bit_cast(bf16x2v, b), acc, false);
 }
 
-__device__ __forceinline__ float dot8_bf16(u32x4 a, u32x4 b, float acc) {
-  acc = dot2_bf16(a.x, b.x, acc);
-  acc = dot2_bf16(a.y, b.y, acc);
-  acc = dot2_bf16(a.z, b.z, acc);
-  acc = dot2_bf16(a.w, b.w, acc);
-  return acc;
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+// The same on a packed fp16 pair (v_dot2_f32_f16).
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v, a), __builtin_bit_cast(f16x2v, b), acc,
+                                false);
+}
+
+// Dot product of 8 packed elements: bf16 (kHalf false) or fp16 (kHalf true).
+template <bool kHalf>
+__device__ __forceinline__ float dot8(u32x4 a, u32x4 b, float acc) {
+  if constexpr (kHalf) {
+    acc = dot2_f16(a.x, b.x, acc);
+    acc = dot2_f16(a.y, b.y, acc);
+    acc = dot2_f16(a.z, b.z, acc);
+    return dot2_f16(a.w, b.w, acc);
+  } else {
+    acc = dot2_bf16(a.x, b.x, acc);
+    acc = dot2_bf16(a.y, b.y, acc);
+    acc = dot2_bf16(a.z, b.z, acc);
+    return dot2_bf16(a.w, b.w, acc);
+  }
 }
 
 // Sum over the 16 lanes of a DPP row: swap neighbours, swap pairs, mirror
@@ -139,6 +154,21 @@ __device__ __forceinline__ uint16_t to_bf16(float f) {
   if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0u) return 0x7FC0;
   u += 0x7FFFu + ((u >> 16) & 1u);
   return static_cast<uint16_t>(u >> 16);
+}
+
+// Element <-> fp32 for the two 16-bit types: the low / high half of a word,
+// and fp32 rounded to nearest even.
+template <bool kHalf>
+__device__ __forceinline__ float elem_lo(uint32_t w) { return kHalf ? half_lo(w) : bf16_lo(w); }
+template <bool kHalf>
+__device__ __forceinline__ float elem_hi(uint32_t w) { return kHalf ? half_hi(w) : bf16_hi(w); }
+template <bool kHalf>
+__device__ __forceinline__ uint16_t from_f32(float f) {
+  if constexpr (kHalf) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  } else {
+    return to_bf16(f);
+  }
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -204,7 +234,7 @@ struct AttnShared {
 // bumps an arrival counter; the last wave to arrive merges and stores them,
 // the others exit at once, so their slots go to the next workgroup instead
 // of idling until the slowest wave's loads return.
-template <int HKV, int G>
+template <int HKV, int G, bool kHalf>
 __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_seq_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
@@ -306,7 +336,7 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
       for (int c = 0; c < NC; ++c) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float d = row16_sum(dot8_bf16(kw[u][c], qf[c][g], 0.f));
+          const float d = row16_sum(dot8<kHalf>(kw[u][c], qf[c][g], 0.f));
           s[u][c][g] = ok[u] ? d * scale_log2 : -INFINITY;
         }
       }
@@ -316,14 +346,14 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
       float v[kAttnUnroll][8];
 #pragma unroll
       for (int u = 0; u < kAttnUnroll; ++u) {
-        v[u][0] = bf16_lo(vw[u][c].x);
-        v[u][1] = bf16_hi(vw[u][c].x);
-        v[u][2] = bf16_lo(vw[u][c].y);
-        v[u][3] = bf16_hi(vw[u][c].y);
-        v[u][4] = bf16_lo(vw[u][c].z);
-        v[u][5] = bf16_hi(vw[u][c].z);
-        v[u][6] = bf16_lo(vw[u][c].w);
-        v[u][7] = bf16_hi(vw[u][c].w);
+        v[u][0] = elem_lo<kHalf>(vw[u][c].x);
+        v[u][1] = elem_hi<kHalf>(vw[u][c].x);
+        v[u][2] = elem_lo<kHalf>(vw[u][c].y);
+        v[u][3] = elem_hi<kHalf>(vw[u][c].y);
+        v[u][4] = elem_lo<kHalf>(vw[u][c].z);
+        v[u][5] = elem_hi<kHalf>(vw[u][c].z);
+        v[u][6] = elem_lo<kHalf>(vw[u][c].w);
+        v[u][7] = elem_hi<kHalf>(vw[u][c].w);
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -445,6 +475,7 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
 constexpr int kReduceWaves = 4;
 constexpr int kReduceThreads = kReduceWaves * kWave;
 
+template <bool kHalf>
 __global__ __launch_bounds__(kReduceThreads) void attn_decode_reduce_kernel(
     const uint32_t* __restrict__ part_acc, const f32x2* __restrict__ part_ml,
     const int32_t* __restrict__ first_part, int64_t capacity, int32_t num_q_heads,
@@ -495,8 +526,8 @@ __global__ __launch_bounds__(kReduceThreads) void attn_decode_reduce_kernel(
     lsum += s_l[w];
   }
   const bool any = lsum > 0.f;
-  const uint32_t packed = static_cast<uint32_t>(to_bf16(any ? ax / lsum : 0.f)) |
-                          (static_cast<uint32_t>(to_bf16(any ? ay / lsum : 0.f)) << 16);
+  const uint32_t packed = static_cast<uint32_t>(from_f32<kHalf>(any ? ax / lsum : 0.f)) |
+                          (static_cast<uint32_t>(from_f32<kHalf>(any ? ay / lsum : 0.f)) << 16);
   *reinterpret_cast<uint32_t*>(out + static_cast<int64_t>(seq) * out_seq_stride +
                                qh * kHeadDim + 2 * lane) = packed;
 }
@@ -505,9 +536,10 @@ using PartialKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const u
                                const int32_t*, int64_t, int32_t, int32_t, const int4*, int32_t,
                                float, uint32_t*, f32x2*);
 
+template <bool kHalf>
 PartialKernel partial_kernel_for(int64_t hkv, int64_t g) {
 #define NKV_ATTN_CASE(H, GG) \
-  if (hkv == H && g == GG) return attn_decode_partial_kernel<H, GG>;
+  if (hkv == H && g == GG) return attn_decode_partial_kernel<H, GG, kHalf>;
   NKV_ATTN_CASE(8, 1)
   NKV_ATTN_CASE(8, 2)
   NKV_ATTN_CASE(4, 1)
@@ -581,9 +613,11 @@ extern "C" int nkv_paged_attention_decode(
     int64_t head_dim, int64_t block_size, int64_t num_blocks, float scale, int32_t dtype,
     void* workspace, int64_t workspace_bytes, void* out, int64_t out_seq_stride, void* stream) {
   using namespace nkv;
-  if (dtype != NKV_DTYPE_BFLOAT16) {
-    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: only bfloat16 is supported");
+  if (dtype != NKV_DTYPE_BFLOAT16 && dtype != NKV_DTYPE_FLOAT16) {
+    return nkv_fail(NKV_E_INVALID,
+                    "nkv_paged_attention_decode: only bfloat16 and float16 are supported");
   }
+  const bool half = dtype == NKV_DTYPE_FLOAT16;
   if (head_dim != kHeadDim) {
     return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: head_dim must be %d", kHeadDim);
   }
@@ -591,7 +625,9 @@ extern "C" int nkv_paged_attention_decode(
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_decode: num_q_heads must be a multiple of num_kv_heads");
   }
-  const PartialKernel kernel = partial_kernel_for(num_kv_heads, num_q_heads / num_kv_heads);
+  const PartialKernel kernel =
+      half ? partial_kernel_for<true>(num_kv_heads, num_q_heads / num_kv_heads)
+           : partial_kernel_for<false>(num_kv_heads, num_q_heads / num_kv_heads);
   if (kernel == nullptr) {
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_decode: unsupported head layout %lld kv x %lld q "
@@ -640,10 +676,15 @@ extern "C" int nkv_paged_attention_decode(
         part_ml);
     if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
   }
-  attn_decode_reduce_kernel<<<dim3(static_cast<unsigned>(num_seqs),
-                                   static_cast<unsigned>(num_q_heads)),
-                              dim3(kReduceThreads), 0, s>>>(
-      part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
-      static_cast<uint16_t*>(out), out_seq_stride);
+  const dim3 reduce_grid(static_cast<unsigned>(num_seqs), static_cast<unsigned>(num_q_heads));
+  if (half) {
+    attn_decode_reduce_kernel<true><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
+        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
+        static_cast<uint16_t*>(out), out_seq_stride);
+  } else {
+    attn_decode_reduce_kernel<false><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
+        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
+        static_cast<uint16_t*>(out), out_seq_stride);
+  }
   return nkv_check_launch("nkv_paged_attention_decode (reduce)");
 }

@@ -10,7 +10,7 @@
 // [0, Lk - Lq + j]; query head h reads kv head h / (Hq / Hkv).
 //
 // The work is GEMM-shaped (each K/V tile serves 128 query rows), so both
-// products run on MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation):
+// products run on MFMA (v_mfma_f32_16x16x32_bf16 / _f16, fp32 accumulation):
 //   * a workgroup owns 128 query rows of one (sequence, kv head): the
 //     (token, query head) pairs of 128 / G consecutive tokens and the
 //     G = Hq / Hkv query heads that share the kv head, token-major;
@@ -24,8 +24,9 @@
 //     only a 4-lane max per row, the P^T operand of O^T = V^T P^T comes
 //     straight from the score registers (the transposing reads deliver V^T
 //     in the same key order), and the output rescale is a per-lane factor;
-//   * P is rounded to bf16 for the second product, as flash attention does,
-//     and the row sum is taken from the same bf16 weights;
+//   * P is rounded to the input type (bf16 or fp16) for the second product,
+//     as flash attention does, and the row sum is taken from the same
+//     rounded weights;
 //   * the query tiles of one kv head run on one XCD (shared L2).
 // Invalid block ids (outside [0, num_blocks), or past the table) drop their
 // keys, as in the decode kernel.
@@ -51,7 +52,7 @@ constexpr int kPfDim = 128;             // head_dim
 constexpr int kPfPlanThreads = 1024;
 
 // Lazy softmax reference (log2 units): weights stay <= 2^8 before the final
-// division, far from fp32 / bf16 overflow.
+// division, far from fp32 / bf16 / fp16 overflow.
 constexpr float kRescaleLog2 = 8.f;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -79,11 +80,30 @@ __device__ __forceinline__ int v_index(int key, int chunk) {
   return key * 16 + (chunk ^ ((key & 7) << 1));
 }
 
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
+// The element type: bf16 (kHalf false) or fp16 (kHalf true), with its 8-
+// and 4-wide vectors and the matching MFMA.
+template <bool kHalf>
+struct Elem {
+  typedef __bf16 T;
+  typedef bf16x8 X8;
+  typedef bf16x4 X4;
+  static __device__ __forceinline__ f32x4 mfma(X8 a, X8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Elem<true> {
+  typedef _Float16 T;
+  typedef f16x8 X8;
+  typedef f16x4 X4;
+  static __device__ __forceinline__ f32x4 mfma(X8 a, X8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
 
 // Max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row's
 // lanes), with the cross-row swaps of gfx950 (no LDS traffic).
@@ -318,7 +338,7 @@ __device__ __forceinline__ TileId tile_of(uint32_t id, int32_t num_kv_heads, int
   return TileId{static_cast<int32_t>(id / num_kv_heads), static_cast<int32_t>(id % num_kv_heads)};
 }
 
-template <int G, bool kWide>
+template <int G, bool kWide, bool kHalf>
 __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_token_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
@@ -328,6 +348,10 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
     const int4* __restrict__ plan, int32_t capacity, int32_t xcd_layout, int32_t num_seqs,
     float scale_log2, uint16_t* __restrict__ out, int64_t out_token_stride) {
   constexpr int kTileTokens = kPfRows / G;
+  typedef Elem<kHalf> E;
+  typedef typename E::T T;
+  typedef typename E::X8 X8;
+  typedef typename E::X4 X4;
   __shared__ u32x4 k_buf0[kTileChunks];
   __shared__ u32x4 k_buf1[kTileChunks];
   __shared__ u32x4 v_buf0[kTileChunks];
@@ -364,7 +388,7 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
                        block_size, block_shift, num_blocks, num_keys};
 
   // Q^T operands (B of S^T = K Q^T): lane holds row m, dims 32 * dc + 8 * g4 .. +8.
-  bf16x8 qb[2][4];
+  X8 qb[2][4];
   int32_t limit[2];  // last visible key of the lane's row, -1 for rows past the tile
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb) {
@@ -378,7 +402,7 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
     for (int dc = 0; dc < 4; ++dc) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (row_ok) v = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * g4);
-      qb[mb][dc] = as_bf16x8(v);
+      qb[mb][dc] = __builtin_bit_cast(X8, v);
     }
   }
 
@@ -393,8 +417,8 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
     acc[db][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const __bf16 one = c16 == 0 ? static_cast<__bf16>(1.f) : static_cast<__bf16>(0.f);
-  const bf16x8 ones = {one, one, one, one, one, one, one, one};
+  const T one = c16 == 0 ? static_cast<T>(1.f) : static_cast<T>(0.f);
+  const X8 ones = {one, one, one, one, one, one, one, one};
 
   // Software pipeline: tile t computes the softmax and PV of tile t and
   // the scores of tile t + 1, so the score MFMAs can issue between the
@@ -430,9 +454,9 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
       s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int dc = 0; dc < 4; ++dc) {
-        const bf16x8 a = as_bf16x8(k_tile[k_index(16 * kb + c16, 4 * dc + g4)]);
-        s[kb][0] = mfma(a, qb[0][dc], s[kb][0]);
-        s[kb][1] = mfma(a, qb[1][dc], s[kb][1]);
+        const X8 a = __builtin_bit_cast(X8, k_tile[k_index(16 * kb + c16, 4 * dc + g4)]);
+        s[kb][0] = E::mfma(a, qb[0][dc], s[kb][0]);
+        s[kb][1] = E::mfma(a, qb[1][dc], s[kb][1]);
       }
     }
   };
@@ -515,17 +539,17 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
 
     // Weights of this tile, then the scores of the next tile.  After the
     // last tile the scores read a stale buffer and are dropped.
-    bf16x8 pb[2][2];
+    X8 pb[2][2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        bf16x8 w;
+        X8 w;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          w[i] = static_cast<__bf16>(
+          w[i] = static_cast<T>(
               __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * c][mb][i], scale_log2, -ref[mb])));
-          w[4 + i] = static_cast<__bf16>(
+          w[4 + i] = static_cast<T>(
               __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * c + 1][mb][i], scale_log2, -ref[mb])));
         }
         pb[c][mb] = w;
@@ -551,15 +575,15 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
       for (int c = 0; c < 2; ++c) {
         const u32x2 lo = v_tr_read(v_cur, 32 * c + tr_key, 16 * db + tr_dim);
         const u32x2 hi = v_tr_read(v_cur, 32 * c + 16 + tr_key, 16 * db + tr_dim);
-        const bf16x8 a = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-        acc[db][0] = mfma(a, pb[c][0], acc[db][0]);
-        acc[db][1] = mfma(a, pb[c][1], acc[db][1]);
+        const X8 a = __builtin_bit_cast(X8, u32x4{lo.x, lo.y, hi.x, hi.y});
+        acc[db][0] = E::mfma(a, pb[c][0], acc[db][0]);
+        acc[db][1] = E::mfma(a, pb[c][1], acc[db][1]);
       }
     }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      acc[8][0] = mfma(ones, pb[c][0], acc[8][0]);
-      acc[8][1] = mfma(ones, pb[c][1], acc[8][1]);
+      acc[8][0] = E::mfma(ones, pb[c][0], acc[8][0]);
+      acc[8][1] = E::mfma(ones, pb[c][1], acc[8][1]);
     }
   };
   for (int32_t tile = 0; tile < num_tiles; tile += 2) {
@@ -580,9 +604,9 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
       const f32x4 v = acc[db][mb];
-      const bf16x4 w = {static_cast<__bf16>(v.x * inv), static_cast<__bf16>(v.y * inv),
-                        static_cast<__bf16>(v.z * inv), static_cast<__bf16>(v.w * inv)};
-      *reinterpret_cast<bf16x4*>(orow + 16 * db + 4 * g4) = w;
+      const X4 w = {static_cast<T>(v.x * inv), static_cast<T>(v.y * inv),
+                    static_cast<T>(v.z * inv), static_cast<T>(v.w * inv)};
+      *reinterpret_cast<X4*>(orow + 16 * db + 4 * g4) = w;
     }
   }
 }
@@ -592,13 +616,13 @@ using PrefillKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const u
                                const int32_t*, const int32_t*, const int4*, int32_t, int32_t,
                                int32_t, float, uint16_t*, int64_t);
 
-template <bool kWide>
+template <bool kWide, bool kHalf>
 PrefillKernel prefill_kernel_for(int64_t group) {
   switch (group) {
-    case 1: return attn_prefill_kernel<1, kWide>;
-    case 2: return attn_prefill_kernel<2, kWide>;
-    case 4: return attn_prefill_kernel<4, kWide>;
-    case 8: return attn_prefill_kernel<8, kWide>;
+    case 1: return attn_prefill_kernel<1, kWide, kHalf>;
+    case 2: return attn_prefill_kernel<2, kWide, kHalf>;
+    case 4: return attn_prefill_kernel<4, kWide, kHalf>;
+    case 8: return attn_prefill_kernel<8, kWide, kHalf>;
     default: return nullptr;
   }
 }
@@ -661,9 +685,11 @@ extern "C" int nkv_paged_attention_prefill(
     int64_t num_blocks, float scale, int32_t dtype, void* out, int64_t out_token_stride,
     void* stream) {
   using namespace nkv;
-  if (dtype != NKV_DTYPE_BFLOAT16) {
-    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: only bfloat16 is supported");
+  if (dtype != NKV_DTYPE_BFLOAT16 && dtype != NKV_DTYPE_FLOAT16) {
+    return nkv_fail(NKV_E_INVALID,
+                    "nkv_paged_attention_prefill: only bfloat16 and float16 are supported");
   }
+  const bool half = dtype == NKV_DTYPE_FLOAT16;
   if (head_dim != kPfDim) {
     return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_prefill: head_dim must be %d", kPfDim);
   }
@@ -714,7 +740,10 @@ extern "C" int nkv_paged_attention_prefill(
   const bool wide = num_blocks * block_size * row_bytes > static_cast<int64_t>(UINT32_MAX);
   const int64_t group = num_q_heads / num_kv_heads;
   const PrefillKernel kernel =
-      wide ? prefill_kernel_for<true>(group) : prefill_kernel_for<false>(group);
+      half ? (wide ? prefill_kernel_for<true, true>(group)
+                   : prefill_kernel_for<false, true>(group))
+           : (wide ? prefill_kernel_for<true, false>(group)
+                   : prefill_kernel_for<false, false>(group));
   int32_t xcd_layout = 0;
   int64_t grid = capacity * num_kv_heads;
   if (num_kv_heads % kXcds == 0) {

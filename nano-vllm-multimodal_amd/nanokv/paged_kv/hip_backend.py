@@ -211,7 +211,8 @@ class HIPPagedKVBackend:
         h // (Hq / Hkv).  The decode call of Attention.forward
         (flash_attn_with_kvcache, attention.py:122-130) with the numerics of
         SDPAAttention's decode branch (attention.py:284-300), without the
-        gather.  q [B, Hq, 128] bf16 -> [B, Hq, 128] bf16."""
+        gather.  q [B, Hq, 128] bf16 or fp16 (the caches' type) -> [B, Hq, 128]
+        in that type."""
         validate_varlen_inputs(key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens)
         if q.ndim != 3 or q.shape[0] != block_tables.shape[0]:
             raise ValueError("q must be [num_seqs, num_q_heads, head_dim] with one row per sequence")
@@ -261,7 +262,8 @@ class HIPPagedKVBackend:
         prefill call of Attention.forward (flash_attn_varlen_func with
         block_table, attention.py:95-116) with the numerics of SDPAAttention's
         prefill (attention.py:226-282).  Request i's queries are rows
-        [cu_seqlens_q[i], cu_seqlens_q[i+1]) of q [Tq, Hq, 128] bf16; its
+        [cu_seqlens_q[i], cu_seqlens_q[i+1]) of q [Tq, Hq, 128] (bf16 or fp16, the
+        caches' type); its
         context is the first Lk = cu_seqlens_k[i+1] - cu_seqlens_k[i] rows
         of its block table, the queries being the last Lq of them.
         ``total_context_tokens`` (= cu_seqlens_k[-1]) is only read by the

@@ -273,8 +273,7 @@ def _paged_attention_decode_impl(q, key_cache, value_cache, block_tables, plan, 
             or block_tables.shape[0] != q.shape[0] or not block_tables.is_contiguous()):
         raise ValueError("block_tables must be a contiguous [num_seqs, width] int32 tensor")
     _require_contiguous_cache("paged KV HIP attention", key_cache, value_cache)
-    if q.dtype != torch.bfloat16 or key_cache.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
-        raise ValueError("paged attention decode supports bfloat16 q, caches and output")
+    _require_attention_dtype("paged attention decode", q, key_cache, value_cache, out)
     if q.ndim != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
         raise ValueError("q must be [num_seqs, num_q_heads, head_dim] with contiguous heads")
     if out.shape != q.shape or out.stride(2) != 1 or out.stride(1) != out.shape[2]:
@@ -295,10 +294,18 @@ def _paged_attention_decode_impl(q, key_cache, value_cache, block_tables, plan, 
         block_tables.data_ptr(), block_tables.shape[1],
         plan.data_ptr() if capacity else None, capacity, first_part.data_ptr(), q.shape[0],
         num_kv_heads, q.shape[1], head_dim, block_size, num_blocks, float(scale),
-        _lib.NKV_DTYPE_BFLOAT16, workspace.data_ptr(), workspace.numel(), out.data_ptr(),
+        DTYPE_CODES[q.dtype], workspace.data_ptr(), workspace.numel(), out.data_ptr(),
         out.stride(0), _stream(device),
     )
     _lib.check(status, "nanovllm_paged_kv::paged_attention_decode")
+
+
+def _require_attention_dtype(what: str, q, key_cache, value_cache, out) -> None:
+    """The attention kernels compute in bf16 or fp16 (fp32 accumulation); q,
+    the caches and the output share that type."""
+    if q.dtype not in (torch.bfloat16, torch.float16) or any(
+            t.dtype != q.dtype for t in (key_cache, value_cache, out)):
+        raise ValueError(f"{what} supports bfloat16 or float16 q, caches and output of one dtype")
 
 
 def _require_cu(name: str, cu: torch.Tensor, num_seqs: int | None = None) -> int:
@@ -336,8 +343,7 @@ def _paged_attention_prefill_impl(q, key_cache, value_cache, block_tables, cu_se
             or block_tables.shape[0] != num_seqs or not block_tables.is_contiguous()):
         raise ValueError("block_tables must be a contiguous [num_seqs, width] int32 tensor")
     _require_contiguous_cache("paged KV HIP prefill attention", key_cache, value_cache)
-    if q.dtype != torch.bfloat16 or key_cache.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
-        raise ValueError("paged attention prefill supports bfloat16 q, caches and output")
+    _require_attention_dtype("paged attention prefill", q, key_cache, value_cache, out)
     if q.ndim != 3 or q.stride(2) != 1 or q.stride(1) != q.shape[2]:
         raise ValueError("q must be [tokens, num_q_heads, head_dim] with contiguous heads")
     if out.shape != q.shape or out.stride(2) != 1 or out.stride(1) != out.shape[2]:
@@ -362,7 +368,7 @@ def _paged_attention_prefill_impl(q, key_cache, value_cache, block_tables, cu_se
         block_tables.data_ptr(), block_tables.shape[1], cu_seqlens_q.data_ptr(),
         cu_seqlens_k.data_ptr(), plan.data_ptr() if plan.shape[0] else None, plan.shape[0],
         num_seqs, num_kv_heads, q.shape[1], head_dim, block_size, num_blocks, float(scale),
-        _lib.NKV_DTYPE_BFLOAT16, out.data_ptr(), out.stride(0), _stream(device),
+        DTYPE_CODES[q.dtype], out.data_ptr(), out.stride(0), _stream(device),
     )
     _lib.check(status, "nanovllm_paged_kv::paged_attention_prefill")
 

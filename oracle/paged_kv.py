@@ -65,14 +65,26 @@ def bf16_words_to_f32(words) -> np.ndarray:
     return (w << 16).view(np.float32)
 
 
-def paged_attention_decode(q, key_cache, value_cache, block_tables, context_lens, scale: float):
+def words_to_f32(words, dtype: str = "bfloat16") -> np.ndarray:
+    """16-bit words of a bfloat16 or float16 tensor -> float32 values (both
+    exact: every bf16 and fp16 value is a float32)."""
+    if dtype == "bfloat16":
+        return bf16_words_to_f32(words)
+    if dtype == "float16":
+        return np.asarray(words).astype(np.uint16).view(np.float16).astype(np.float32)
+    raise ValueError(f"unsupported element type {dtype}")
+
+
+def paged_attention_decode(q, key_cache, value_cache, block_tables, context_lens, scale: float,
+                           dtype: str = "bfloat16"):
     """SDPAAttention's decode branch in float32 (nanovllm/layers/attention.py:
     284-300): per request, gather K and V of its context (the pytorch
     backend's gather, pytorch_backend.py:40-50), then
     softmax(scale * q K^T) V with grouped-query heads: query head h reads kv
     head h // (Hq / Hkv), as scaled_dot_product_attention(enable_gqa=True)
-    does (attention.py:194-203).  q [B, Hq, D] float32; caches hold bf16
-    words ([NB, BS, Hkv, D] int16); an empty context yields zeros."""
+    does (attention.py:194-203).  q [B, Hq, D] float32; caches hold the
+    16-bit words of a ``dtype`` tensor ([NB, BS, Hkv, D] int16); an empty
+    context yields zeros."""
     q = np.asarray(q, dtype=np.float32)
     b, hq, d = q.shape
     hkv = key_cache.shape[2]
@@ -81,8 +93,8 @@ def paged_attention_decode(q, key_cache, value_cache, block_tables, context_lens
     for i, length in enumerate(np.asarray(context_lens).tolist()):
         if length == 0:
             continue
-        k = bf16_words_to_f32(gather(key_cache, block_tables[i], int(length)))
-        v = bf16_words_to_f32(gather(value_cache, block_tables[i], int(length)))
+        k = words_to_f32(gather(key_cache, block_tables[i], int(length)), dtype)
+        v = words_to_f32(gather(value_cache, block_tables[i], int(length)), dtype)
         for h in range(hq):
             kv = h // group
             scores = (k[:, kv, :] @ q[i, h]) * np.float32(scale)
@@ -94,7 +106,7 @@ def paged_attention_decode(q, key_cache, value_cache, block_tables, context_lens
 
 
 def paged_attention_prefill(q, cu_seqlens_q, key_cache, value_cache, block_tables, cu_seqlens_k,
-                            scale: float):
+                            scale: float, dtype: str = "bfloat16"):
     """Prefill attention over the paged cache in float32, as the reference's
     prefill computes it when block tables are present: the Flash path reads
     the cache through block_table (nanovllm/layers/attention.py:95-116,
@@ -104,8 +116,8 @@ def paged_attention_prefill(q, cu_seqlens_q, key_cache, value_cache, block_table
     [cu_seqlens_q[i], cu_seqlens_q[i+1]) (Lq of them) and context rows
     [0, Lk), Lk = cu_seqlens_k[i+1] - cu_seqlens_k[i] >= Lq; its query j sits
     at position Lk - Lq + j and attends keys [0, Lk - Lq + j].  Query head h
-    reads kv head h // (Hq / Hkv).  q [Tq, Hq, D] float32, caches bf16 words
-    [NB, BS, Hkv, D]; returns [Tq, Hq, D] float32."""
+    reads kv head h // (Hq / Hkv).  q [Tq, Hq, D] float32, caches the 16-bit
+    words of a ``dtype`` tensor [NB, BS, Hkv, D]; returns [Tq, Hq, D] float32."""
     q = np.asarray(q, dtype=np.float32)
     tq, hq, d = q.shape
     hkv = key_cache.shape[2]
@@ -120,8 +132,8 @@ def paged_attention_prefill(q, cu_seqlens_q, key_cache, value_cache, block_table
             continue
         if lk < lq:
             raise ValueError("every request needs at least as many keys as queries")
-        k = bf16_words_to_f32(gather(key_cache, block_tables[i], lk))
-        v = bf16_words_to_f32(gather(value_cache, block_tables[i], lk))
+        k = words_to_f32(gather(key_cache, block_tables[i], lk), dtype)
+        v = words_to_f32(gather(value_cache, block_tables[i], lk), dtype)
         visible = np.arange(lk)[None, :] <= (lk - lq + np.arange(lq))[:, None]  # [Lq, Lk]
         for h in range(hq):
             kv = h // group

@@ -35,7 +35,7 @@ def check_close(got: torch.Tensor, ref: np.ndarray, what: str) -> None:
     assert not bad.any(), f"{what}: {int(bad.sum())} elements off, max err {np.abs(g - ref).max():.3e}"
 
 
-def build_case(device, hkv, g, bs, lens, seed, q_pad_heads=0):
+def build_case(device, hkv, g, bs, lens, seed, q_pad_heads=0, dtype=torch.bfloat16):
     gen = torch.Generator().manual_seed(seed)
     b = len(lens)
     need = [-(-int(n) // bs) for n in lens]
@@ -47,10 +47,10 @@ def build_case(device, hkv, g, bs, lens, seed, q_pad_heads=0):
     for i, n in enumerate(need):
         tables[i, :n] = perm[cursor:cursor + n]
         cursor += n
-    kc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16)
-    vc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16)
+    kc = torch.randn(nb, bs, hkv, 128, generator=gen).to(dtype)
+    vc = torch.randn(nb, bs, hkv, 128, generator=gen).to(dtype)
     hq = hkv * g
-    q_full = torch.randn(b, hq + q_pad_heads, 128, generator=gen).to(torch.bfloat16)
+    q_full = torch.randn(b, hq + q_pad_heads, 128, generator=gen).to(dtype)
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     dev = dict(
         kc=kc.to(device), vc=vc.to(device), q=q_full.to(device)[:, :hq],
@@ -76,6 +76,21 @@ def test_decode_attention_matches_oracle(backend, gpu_device, hkv, g, bs):
                                         host["lens"], scale)
     check_close(out, ref, f"hkv={hkv} g={g} bs={bs}")
     assert torch.all(out[0] == 0), "an empty context must give zeros"
+
+
+@pytest.mark.parametrize("hkv,g,bs", [(8, 2, 16), (2, 8, 256), (1, 1, 4), (4, 2, 24)])
+def test_decode_attention_float16_matches_oracle(backend, gpu_device, hkv, g, bs):
+    """float16 q and caches: v_dot2 on fp16 pairs, fp16 output; the same
+    tolerance holds (fp16 rounds to 2^-11)."""
+    lens = [0, 1, bs - 1, bs, bs + 1, 3 * bs + 7, 2, 5 * bs, 17, 1]
+    dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=hkv + g + bs,
+                                  dtype=torch.float16)
+    out = backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev["tables"], dev["cu"],
+                                         total, 0.0884)
+    assert out.dtype == torch.float16
+    ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], host["tables"],
+                                        host["lens"], 0.0884, dtype="float16")
+    check_close(out, ref, f"fp16 hkv={hkv} g={g} bs={bs}")
 
 
 def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):

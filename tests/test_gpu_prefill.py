@@ -38,7 +38,8 @@ def check_close(got: torch.Tensor, ref: np.ndarray, ref_abs: np.ndarray, what: s
     assert not bad.any(), f"{what}: {int(bad.sum())} elements off, max err {np.abs(g - ref).max():.3e}"
 
 
-def build_case(device, hkv, g, bs, q_lens, k_lens, seed, q_extra_heads=0, spare_blocks=5):
+def build_case(device, hkv, g, bs, q_lens, k_lens, seed, q_extra_heads=0, spare_blocks=5,
+               dtype=torch.bfloat16):
     gen = torch.Generator().manual_seed(seed)
     b = len(q_lens)
     need = [-(-int(n) // bs) for n in k_lens]
@@ -50,19 +51,20 @@ def build_case(device, hkv, g, bs, q_lens, k_lens, seed, q_extra_heads=0, spare_
     for i, n in enumerate(need):
         tables[i, :n] = perm[cursor:cursor + n]
         cursor += n
-    kc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16)
-    vc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16)
+    kc = torch.randn(nb, bs, hkv, 128, generator=gen).to(dtype)
+    vc = torch.randn(nb, bs, hkv, 128, generator=gen).to(dtype)
     hq = hkv * g
     cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     cu_k = np.concatenate([[0], np.cumsum(k_lens)]).astype(np.int32)
-    q_full = torch.randn(int(cu_q[-1]), hq + q_extra_heads, 128, generator=gen).to(torch.bfloat16)
+    q_full = torch.randn(int(cu_q[-1]), hq + q_extra_heads, 128, generator=gen).to(dtype)
     dev = dict(
         kc=kc.to(device), vc=vc.to(device), q=q_full.to(device)[:, :hq],
         tables=torch.from_numpy(tables).to(device), cu_q=torch.from_numpy(cu_q).to(device),
         cu_k=torch.from_numpy(cu_k).to(device),
     )
     host = dict(q=q_full[:, :hq].float().numpy(), kc=kc.view(torch.int16).numpy(),
-                vc=vc.view(torch.int16).numpy(), tables=tables, cu_q=cu_q, cu_k=cu_k)
+                vc=vc.view(torch.int16).numpy(), tables=tables, cu_q=cu_q, cu_k=cu_k,
+                dtype=str(dtype).removeprefix("torch."))
     return dev, host
 
 
@@ -75,10 +77,10 @@ def reference(host, scale, tables=None):
     """(fp32 attention, the same attention over |V|)."""
     tables = host["tables"] if tables is None else tables
     ref = oracle.paged_attention_prefill(host["q"], host["cu_q"], host["kc"], host["vc"], tables,
-                                         host["cu_k"], scale)
-    v_abs = host["vc"] & np.int16(0x7FFF)  # bf16 words with the sign cleared
+                                         host["cu_k"], scale, dtype=host["dtype"])
+    v_abs = host["vc"] & np.int16(0x7FFF)  # bf16 / fp16 words with the sign cleared
     ref_abs = oracle.paged_attention_prefill(host["q"], host["cu_q"], host["kc"], v_abs, tables,
-                                             host["cu_k"], scale)
+                                             host["cu_k"], scale, dtype=host["dtype"])
     return ref, ref_abs
 
 
@@ -124,6 +126,20 @@ def check_plan(plan, q_lens, k_lens, tile, longest_first):
         assert visible == sorted(visible, reverse=True)
     else:
         assert order == by_sequence
+
+
+@pytest.mark.parametrize("hkv,g,bs", [(8, 2, 256), (2, 4, 16), (1, 1, 24)])
+def test_prefill_float16_matches_oracle(backend, gpu_device, hkv, g, bs):
+    """float16 q and caches: the f16 MFMA, weights rounded to fp16, fp16
+    output; the same tolerance holds (fp16 rounds to 2^-11)."""
+    q_lens = [1, 37, 200, 64, 0, 130]
+    k_lens = [1, 37, 333, 64 + 3 * bs + 5, 12, 130]
+    dev, host = build_case(gpu_device, hkv, g, bs, q_lens, k_lens, seed=hkv + g + bs,
+                           dtype=torch.float16)
+    scale = 1.0 / math.sqrt(128)
+    out = run(backend, dev, scale)
+    assert out.dtype == torch.float16
+    check_close(out, *reference(host, scale), f"fp16 hkv={hkv} g={g} bs={bs}")
 
 
 def test_plan_tiles_cover_every_query(backend, gpu_device):
@@ -331,19 +347,21 @@ def test_flash_varlen_contiguous_keys_matches_oracle(gpu_device):
     check_close(out, *reference(host, 0.1), "flash varlen contiguous")
 
 
-def test_flash_with_kvcache_matches_decode_oracle(gpu_device):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_flash_with_kvcache_matches_decode_oracle(gpu_device, dtype):
     """attention.py:122-130: flash_attn_with_kvcache(q.unsqueeze(1), k_cache,
-    v_cache, cache_seqlens=context_lens, block_table=..., causal=True)."""
+    v_cache, cache_seqlens=context_lens, block_table=..., causal=True), for
+    bf16 and fp16 models."""
     from nanokv.flash import flash_attn_with_kvcache
 
     k_lens = [1, 300, 17, 64]
-    dev, host = build_case(gpu_device, 8, 2, 16, [1] * 4, k_lens, seed=37)
+    dev, host = build_case(gpu_device, 8, 2, 16, [1] * 4, k_lens, seed=37, dtype=dtype)
     lens = torch.tensor(k_lens, dtype=torch.int32, device=gpu_device)
     out = flash_attn_with_kvcache(dev["q"].unsqueeze(1), dev["kc"], dev["vc"], cache_seqlens=lens,
                                   block_table=dev["tables"], softmax_scale=0.088, causal=True)
-    assert out.shape == (4, 1, 16, 128)
+    assert out.shape == (4, 1, 16, 128) and out.dtype == dtype
     ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], host["tables"],
-                                        np.array(k_lens), 0.088)
+                                        np.array(k_lens), 0.088, dtype=host["dtype"])
     g = out[:, 0].float().cpu().numpy()
     assert not (np.abs(g - ref) > 1e-3 + 1e-2 * np.abs(ref)).any()
 

@@ -128,3 +128,40 @@ def test_planted_mistakes_are_caught():
     assert not np.allclose(wrong_heads, good, atol=1e-3)
     right = np.stack([[attend(j, h, h // 2, 10 - 4 + j) for h in range(4)] for j in range(4)])
     np.testing.assert_allclose(right, good, rtol=1e-5, atol=1e-6)
+
+
+def test_float16_words_and_oracle_equal_torch():
+    """The fp16 path: the word conversion equals torch's float16 -> float32
+    for every finite and special pattern, and the oracle on float16 caches
+    equals SDPA with the prefix-causal mask on the same values, taken from
+    torch directly."""
+    words = np.arange(-32768, 32768, dtype=np.int64).astype(np.int16)
+    expect = torch.from_numpy(words).view(torch.float16).float().numpy()
+    got = oracle.words_to_f32(words, "float16")
+    both_nan = np.isnan(got) & np.isnan(expect)
+    np.testing.assert_array_equal(got[~both_nan], expect[~both_nan])
+
+    q_lens, k_lens = [3, 5, 2], [9, 5, 8]
+    gen = torch.Generator().manual_seed(5)
+    nb, bs, hkv, g, d = 12, 4, 2, 2, 16
+    kc = torch.randn(nb, bs, hkv, d, generator=gen).to(torch.float16)
+    vc = torch.randn(nb, bs, hkv, d, generator=gen).to(torch.float16)
+    cu_q = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(k_lens)]).astype(np.int32)
+    q = torch.randn(int(cu_q[-1]), hkv * g, d, generator=gen).to(torch.float16).float()
+    tables = np.array([[0, 1, 2], [3, 4, -1], [5, 6, -1]], np.int32)
+    scale = 1.0 / math.sqrt(d)
+    out = oracle.paged_attention_prefill(q.numpy(), cu_q, kc.view(torch.int16).numpy(),
+                                         vc.view(torch.int16).numpy(), tables, cu_k, scale,
+                                         dtype="float16")
+    for i, (lq, lk) in enumerate(zip(q_lens, k_lens)):
+        rows = [int(tables[i][t // bs]) * bs + t % bs for t in range(lk)]
+        k = kc.flatten(0, 1)[rows].float()
+        v = vc.flatten(0, 1)[rows].float()
+        mask = torch.arange(lk)[None, :] <= (torch.arange(lq) + (lk - lq))[:, None]
+        expected = F.scaled_dot_product_attention(
+            q[cu_q[i]:cu_q[i + 1]].transpose(0, 1).unsqueeze(0),
+            k.transpose(0, 1).unsqueeze(0).contiguous(), v.transpose(0, 1).unsqueeze(0).contiguous(),
+            attn_mask=mask.unsqueeze(0).unsqueeze(0), scale=scale, enable_gqa=True,
+        )[0].transpose(0, 1)
+        np.testing.assert_allclose(out[cu_q[i]:cu_q[i + 1]], expected.numpy(), rtol=1e-5, atol=1e-6)
