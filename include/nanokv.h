@@ -241,7 +241,8 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  * for query head h, G = num_q_heads / num_kv_heads (kv head h / G), in fp32
  * with a result in the input type.  An empty context yields zeros.  dtype
  * NKV_DTYPE_BFLOAT16 or NKV_DTYPE_FLOAT16 (q, caches and out alike),
- * head_dim 128, num_kv_heads in {1,2,4,8}, at most 16 query heads.
+ * head_dim 128, num_kv_heads in {1,2,4,8}, G <= 8 (G <= 4 with 8 kv
+ * heads), so at most 32 query heads.
  *
  * Replaces: the decode call flash_attn_with_kvcache(q, k_cache, v_cache,
  *   cache_seqlens=context_lens, block_table=block_tables, softmax_scale,
@@ -288,7 +289,7 @@ int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
  * Paged-attention prefill: causal attention of each sequence's chunk of
  * query tokens over its context, read straight from the paged cache
  * (head_dim 128, bfloat16 or float16 for q, caches and out alike, query
- * heads per kv head G = 1, 2, 4 or 8).
+ * heads per kv head G = 1 to 8).
  * Request i has query rows [cu_seqlens_q[i], cu_seqlens_q[i+1]) (Lq) and
  * context rows [0, Lk), Lk = cu_seqlens_k[i+1] - cu_seqlens_k[i] >= Lq;
  * query j sees keys [0, Lk - Lq + j]; query head h reads kv head h / G.

@@ -64,7 +64,7 @@ constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kHeadDim = 128;
 constexpr int kHeadBytes = kHeadDim * 2;  // bf16
 constexpr int kAttnUnroll = NKV_ATTN_UNROLL;
-constexpr int kMaxQHeads = 16;
+constexpr int kMaxQHeads = 32;  // the waves' LDS merge buffer: 4 KiB per query head
 constexpr int kEntryRows = NKV_ATTN_ENTRY_ROWS;
 constexpr int kMaxEntryBlocks = 64;  // blocks one entry may span
 constexpr int kPlanThreads = 1024;
@@ -540,18 +540,35 @@ template <bool kHalf>
 PartialKernel partial_kernel_for(int64_t hkv, int64_t g) {
 #define NKV_ATTN_CASE(H, GG) \
   if (hkv == H && g == GG) return attn_decode_partial_kernel<H, GG, kHalf>;
+  // Every layout with G <= 8 query heads per kv head (G <= 4 with 8 kv
+  // heads: a lane keeps 2 kv heads x G query heads in registers).
   NKV_ATTN_CASE(8, 1)
   NKV_ATTN_CASE(8, 2)
+  NKV_ATTN_CASE(8, 3)
+  NKV_ATTN_CASE(8, 4)
   NKV_ATTN_CASE(4, 1)
   NKV_ATTN_CASE(4, 2)
+  NKV_ATTN_CASE(4, 3)
   NKV_ATTN_CASE(4, 4)
+  NKV_ATTN_CASE(4, 5)
+  NKV_ATTN_CASE(4, 6)
+  NKV_ATTN_CASE(4, 7)
+  NKV_ATTN_CASE(4, 8)
   NKV_ATTN_CASE(2, 1)
   NKV_ATTN_CASE(2, 2)
+  NKV_ATTN_CASE(2, 3)
   NKV_ATTN_CASE(2, 4)
+  NKV_ATTN_CASE(2, 5)
+  NKV_ATTN_CASE(2, 6)
+  NKV_ATTN_CASE(2, 7)
   NKV_ATTN_CASE(2, 8)
   NKV_ATTN_CASE(1, 1)
   NKV_ATTN_CASE(1, 2)
+  NKV_ATTN_CASE(1, 3)
   NKV_ATTN_CASE(1, 4)
+  NKV_ATTN_CASE(1, 5)
+  NKV_ATTN_CASE(1, 6)
+  NKV_ATTN_CASE(1, 7)
   NKV_ATTN_CASE(1, 8)
 #undef NKV_ATTN_CASE
   return nullptr;
@@ -631,9 +648,8 @@ extern "C" int nkv_paged_attention_decode(
   if (kernel == nullptr) {
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_decode: unsupported head layout %lld kv x %lld q "
-                    "(kv heads 1/2/4/8, at most %d query heads)",
-                    static_cast<long long>(num_kv_heads), static_cast<long long>(num_q_heads),
-                    kMaxQHeads);
+                    "(kv heads 1/2/4/8, at most 8 query heads per kv head, 4 with 8 kv heads)",
+                    static_cast<long long>(num_kv_heads), static_cast<long long>(num_q_heads));
   }
   if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX ||
       block_size <= 0 || num_blocks < 0 || num_blocks * block_size > INT32_MAX ||

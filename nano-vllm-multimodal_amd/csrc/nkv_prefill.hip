@@ -621,7 +621,11 @@ PrefillKernel prefill_kernel_for(int64_t group) {
   switch (group) {
     case 1: return attn_prefill_kernel<1, kWide, kHalf>;
     case 2: return attn_prefill_kernel<2, kWide, kHalf>;
+    case 3: return attn_prefill_kernel<3, kWide, kHalf>;
     case 4: return attn_prefill_kernel<4, kWide, kHalf>;
+    case 5: return attn_prefill_kernel<5, kWide, kHalf>;
+    case 6: return attn_prefill_kernel<6, kWide, kHalf>;
+    case 7: return attn_prefill_kernel<7, kWide, kHalf>;
     case 8: return attn_prefill_kernel<8, kWide, kHalf>;
     default: return nullptr;
   }
@@ -631,7 +635,9 @@ PrefillKernel prefill_kernel_for(int64_t group) {
 }  // namespace nkv
 
 extern "C" int64_t nkv_prefill_tile_tokens(int64_t group) {
-  return group == 1 || group == 2 || group == 4 || group == 8 ? nkv::kPfRows / group : 0;
+  // 128 query rows per workgroup: 128 / G whole tokens (with G = 3, 5, 6
+  // or 7 the last 128 % G rows idle).
+  return group >= 1 && group <= 8 ? nkv::kPfRows / group : 0;
 }
 
 extern "C" int64_t nkv_prefill_plan_capacity(int64_t total_q_tokens, int64_t num_seqs,
@@ -648,7 +654,7 @@ extern "C" int nkv_build_prefill_plan(const int32_t* cu_seqlens_q, const int32_t
   const int64_t tile = nkv_prefill_tile_tokens(group);
   if (tile == 0) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: query heads per kv head must be "
-                                   "1, 2, 4 or 8 (got %lld)", static_cast<long long>(group));
+                                   "1 to 8 (got %lld)", static_cast<long long>(group));
   }
   if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_prefill_plan: num_seqs=%lld or capacity=%lld "
@@ -700,7 +706,7 @@ extern "C" int nkv_paged_attention_prefill(
   }
   if (nkv_prefill_tile_tokens(num_q_heads / num_kv_heads) == 0) {
     return nkv_fail(NKV_E_INVALID,
-                    "nkv_paged_attention_prefill: %lld query heads per kv head (1, 2, 4 or 8 "
+                    "nkv_paged_attention_prefill: %lld query heads per kv head (1 to 8 "
                     "supported)", static_cast<long long>(num_q_heads / num_kv_heads));
   }
   if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX ||

@@ -323,7 +323,7 @@ def _build_prefill_plan_impl(cu_seqlens_q, cu_seqlens_k, total_q_tokens: int, gr
     library = _lib.load_library()
     capacity = int(library.nkv_prefill_plan_capacity(total_q_tokens, num_seqs, group))
     if capacity == 0 and total_q_tokens > 0:
-        raise ValueError("prefill attention supports 1, 2, 4 or 8 query heads per kv head")
+        raise ValueError("prefill attention supports 1 to 8 query heads per kv head")
     plan = torch.empty((capacity, 4), dtype=torch.int32, device=device)
     status = library.nkv_build_prefill_plan(
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), num_seqs, group,

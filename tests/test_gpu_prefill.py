@@ -88,12 +88,15 @@ def reference(host, scale, tables=None):
     (8, 2, 256), (8, 2, 16), (2, 8, 16), (4, 4, 32), (1, 1, 16), (2, 4, 8), (8, 1, 256), (1, 8, 64),
     (16, 1, 16), (3, 2, 16), (6, 1, 32),
     (8, 2, 24), (4, 2, 100),  # block sizes that are not powers of two
+    (4, 7, 16), (8, 4, 256), (8, 3, 32), (2, 5, 16), (1, 6, 64),  # Qwen2.5-VL-7B, Qwen3-VL-8B, ...
 ])
 def test_prefill_matches_oracle(backend, gpu_device, hkv, g, bs):
     """Full prompts (Lq == Lk), continuation chunks over a cached prefix
     (Lk > Lq), single-token chunks, chunks of several query tiles, ragged
     last blocks, and an empty request.  Block sizes of 24 and 100 take the
-    division path of the row map (the others shift).  The kv head counts
+    division path of the row map (the others shift).  Query heads per kv
+    head from 1 to 8; with 3, 5, 6 or 7 the last rows of each workgroup
+    idle.  The kv head counts
     cover each mapping of workgroups to XCDs: multiples of 8 (8, 16),
     divisors of 8 (1, 2, 4; the plan's length is not a multiple of 8 / H)
     and neither (3, 6)."""
@@ -275,9 +278,9 @@ def test_cache_over_4gib(backend, gpu_device):
 
 def test_unsupported_layouts_raise(backend, gpu_device):
     dev, _ = build_case(gpu_device, 3, 1, 16, [4], [4], seed=1)
-    q3 = torch.zeros((4, 9, 128), dtype=torch.bfloat16, device=gpu_device)  # G = 3
+    q9 = torch.zeros((4, 27, 128), dtype=torch.bfloat16, device=gpu_device)  # G = 9
     with pytest.raises((ValueError, RuntimeError)):
-        backend.paged_attention_prefill(q3, dev["kc"], dev["vc"], dev["tables"], dev["cu_q"],
+        backend.paged_attention_prefill(q9, dev["kc"], dev["vc"], dev["tables"], dev["cu_q"],
                                         dev["cu_k"], 0.1)
 
 
