@@ -234,7 +234,9 @@ struct AttnShared {
 // bumps an arrival counter; the last wave to arrive merges and stores them,
 // the others exit at once, so their slots go to the next workgroup instead
 // of idling until the slowest wave's loads return.
-template <int HKV, int G, bool kHalf>
+// kRowHeads: kv heads in a cache row (HKV unless the layout is run in parts
+// of HKV heads).
+template <int HKV, int G, bool kHalf, int kRowHeads = HKV>
 __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_seq_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
   constexpr int HQ = HKV * G;
   constexpr int NC = HKV >= 4 ? HKV / 4 : 1;   // kv heads per lane per row
   constexpr int TPI = HKV >= 4 ? 1 : 4 / HKV;  // rows per wavefront load
-  constexpr int kRowBytes = HKV * kHeadBytes;
+  constexpr int kRowBytes = kRowHeads * kHeadBytes;
   static_assert(HQ <= kMaxQHeads && NC * G <= 8, "unsupported head layout");
   __shared__ AttnShared<HQ> sh;
 
@@ -573,6 +575,18 @@ PartialKernel partial_kernel_for(int64_t hkv, int64_t g) {
 #undef NKV_ATTN_CASE
   return nullptr;
 }
+// 8 kv heads with 5 to 8 query heads each (40 to 64 query heads): run as
+// two parts of 4 kv heads, each reading its half of every cache row.
+template <bool kHalf>
+PartialKernel split_partial_kernel_for(int64_t g) {
+  switch (g) {
+    case 5: return attn_decode_partial_kernel<4, 5, kHalf, 8>;
+    case 6: return attn_decode_partial_kernel<4, 6, kHalf, 8>;
+    case 7: return attn_decode_partial_kernel<4, 7, kHalf, 8>;
+    case 8: return attn_decode_partial_kernel<4, 8, kHalf, 8>;
+    default: return nullptr;
+  }
+}
 
 }  // namespace
 }  // namespace nkv
@@ -642,13 +656,18 @@ extern "C" int nkv_paged_attention_decode(
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_decode: num_q_heads must be a multiple of num_kv_heads");
   }
-  const PartialKernel kernel =
-      half ? partial_kernel_for<true>(num_kv_heads, num_q_heads / num_kv_heads)
-           : partial_kernel_for<false>(num_kv_heads, num_q_heads / num_kv_heads);
+  const int64_t group = num_q_heads / num_kv_heads;
+  PartialKernel kernel = half ? partial_kernel_for<true>(num_kv_heads, group)
+                              : partial_kernel_for<false>(num_kv_heads, group);
+  int64_t parts = 1;  // launches, each over num_kv_heads / parts kv heads
+  if (kernel == nullptr && num_kv_heads == 8) {
+    kernel = half ? split_partial_kernel_for<true>(group) : split_partial_kernel_for<false>(group);
+    parts = 2;
+  }
   if (kernel == nullptr) {
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_decode: unsupported head layout %lld kv x %lld q "
-                    "(kv heads 1/2/4/8, at most 8 query heads per kv head, 4 with 8 kv heads)",
+                    "(kv heads 1/2/4/8, at most 8 query heads per kv head)",
                     static_cast<long long>(num_kv_heads), static_cast<long long>(num_q_heads));
   }
   if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX ||
@@ -680,27 +699,38 @@ extern "C" int nkv_paged_attention_decode(
                     "and out rows 4-byte aligned");
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  auto* part_acc = static_cast<uint32_t*>(workspace);  // fp16 pairs
-  auto* part_ml = reinterpret_cast<f32x2*>(part_acc + capacity * num_q_heads * head_dim / 2);
   const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
-  if (capacity > 0) {
-    kernel<<<dim3(static_cast<unsigned>(capacity)), dim3(kAttnThreads), 0, s>>>(
-        static_cast<const uint16_t*>(q), q_seq_stride, static_cast<const uint8_t*>(key_cache),
-        static_cast<const uint8_t*>(value_cache), block_tables, table_stride,
-        static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
-        static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2, part_acc,
-        part_ml);
-    if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
+  // Each part covers num_kv_heads / parts kv heads and their query heads:
+  // q, out and the caches advance by that many heads; the parts run one
+  // after the other on the stream and share the workspace.
+  const int64_t part_q_heads = num_q_heads / parts;
+  auto* part_acc = static_cast<uint32_t*>(workspace);  // fp16 pairs
+  auto* part_ml = reinterpret_cast<f32x2*>(part_acc + capacity * part_q_heads * head_dim / 2);
+  for (int64_t p = 0; p < parts; ++p) {
+    const int64_t q_off = p * part_q_heads * head_dim;                        // elements
+    const int64_t kv_off = p * (num_kv_heads / parts) * head_dim * 2;         // bytes
+    if (capacity > 0) {
+      kernel<<<dim3(static_cast<unsigned>(capacity)), dim3(kAttnThreads), 0, s>>>(
+          static_cast<const uint16_t*>(q) + q_off, q_seq_stride,
+          static_cast<const uint8_t*>(key_cache) + kv_off,
+          static_cast<const uint8_t*>(value_cache) + kv_off, block_tables, table_stride,
+          static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
+          static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2, part_acc,
+          part_ml);
+      if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
+    }
+    const dim3 reduce_grid(static_cast<unsigned>(num_seqs), static_cast<unsigned>(part_q_heads));
+    uint16_t* part_out = static_cast<uint16_t*>(out) + q_off;
+    if (half) {
+      attn_decode_reduce_kernel<true><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
+          part_acc, part_ml, first_part, capacity, static_cast<int32_t>(part_q_heads), part_out,
+          out_seq_stride);
+    } else {
+      attn_decode_reduce_kernel<false><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
+          part_acc, part_ml, first_part, capacity, static_cast<int32_t>(part_q_heads), part_out,
+          out_seq_stride);
+    }
+    if (int rc = nkv_check_launch("nkv_paged_attention_decode (reduce)")) return rc;
   }
-  const dim3 reduce_grid(static_cast<unsigned>(num_seqs), static_cast<unsigned>(num_q_heads));
-  if (half) {
-    attn_decode_reduce_kernel<true><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
-        static_cast<uint16_t*>(out), out_seq_stride);
-  } else {
-    attn_decode_reduce_kernel<false><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
-        static_cast<uint16_t*>(out), out_seq_stride);
-  }
-  return nkv_check_launch("nkv_paged_attention_decode (reduce)");
+  return NKV_OK;
 }
