@@ -241,8 +241,10 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  * for query head h, G = num_q_heads / num_kv_heads (kv head h / G), in fp32
  * with a result in the input type.  An empty context yields zeros.  dtype
  * NKV_DTYPE_BFLOAT16 or NKV_DTYPE_FLOAT16 (q, caches and out alike),
- * head_dim 128, num_kv_heads in {1,2,4,8}, G <= 8 (with 8 kv heads and
- * G > 4 it runs as two launches of 4 kv heads).
+ * head_dim 128, any num_kv_heads, G <= 16.  G = 1 or 2 with 1, 2, 4 or 8
+ * kv heads runs on the VALU kernel; every other layout runs on the MFMA
+ * kernel, which rounds the softmax weights to the input type before the
+ * product with V, as flash attention does.
  *
  * Replaces: the decode call flash_attn_with_kvcache(q, k_cache, v_cache,
  *   cache_seqlens=context_lens, block_table=block_tables, softmax_scale,

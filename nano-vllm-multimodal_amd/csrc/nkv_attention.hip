@@ -9,29 +9,33 @@
 //
 // Split-K ("flash decoding"): the context of every sequence is cut into
 // entries of up to attention_entry_rows(block_size) rows (768 by default,
-// whole blocks), one workgroup per entry computes softmax partials for every
-// query head (reference max m, weight sum l, unnormalised output), and a
-// reduce kernel merges the partials of each (sequence, query head).
+// whole blocks), one workgroup per entry computes softmax partials (reference
+// max m, weight sum l, unnormalised output), and a reduce kernel merges the
+// partials of each (sequence, query head).  Two kernels write the partials:
 //
-// Mapping inside a workgroup (8 waves, head_dim 128, bf16 or fp16):
+// VALU kernel, G = Hq / Hkv = 1 or 2 (Hkv = 1, 2, 4, 8), one workgroup per
+// entry for all heads (8 waves):
 //   * the entry's cache rows are resolved once through the block table into
 //     LDS (invalid block ids give rows that are skipped);
 //   * a 16-lane DPP row owns one (row, kv head): each lane holds 8 dims
 //     (16 bytes), so a wavefront instruction reads 1 KiB of consecutive
 //     cache bytes (coalesced, non-temporal); the waves take interleaved
 //     groups of rows, so the workgroup sweeps its rows as one front;
-//   * q.k for the G = Hq/Hkv query heads of that kv head is 4 v_dot2 on
-//     packed bf16 / fp16 pairs plus a 4-step DPP row sum (fp32);
+//   * q.k for the G query heads of that kv head is 4 v_dot2 on packed
+//     bf16 / fp16 pairs plus a 4-step DPP row sum (fp32);
 //   * an online softmax in fp32 with exp2 (scale * log2 e folded in);
 //   * the waves merge in LDS without a barrier: the last one to arrive
 //     stores the entry's partials (fp16 sums with a power-of-two scale).
-// Decode attention moves ~2 bytes per FLOP pair and has only G = 1..8 query
-// rows per kv head, so it is bound by HBM reads; an MFMA tile (16 rows)
-// would idle most of its lanes, while the VALU work here stays under the
-// memory time and overlaps it across waves.
+// At G <= 2 its VALU work stays under the memory time.
+//
+// MFMA kernel, G = 3..16 and any other kv-head count: one workgroup per
+// (entry, kv head), the G query heads as the columns of 16x16 MFMA tiles
+// (see attn_decode_mfma_kernel); the VALU cost of 2 G FLOPs per cache byte
+// would outrun the memory time from G = 3 on.
 #include <cmath>
 
 #include "nkv_common.h"
+#include "nkv_mfma.h"
 
 namespace nkv {
 namespace {
@@ -64,7 +68,7 @@ constexpr int kAttnThreads = kAttnWaves * kWave;
 constexpr int kHeadDim = 128;
 constexpr int kHeadBytes = kHeadDim * 2;  // bf16
 constexpr int kAttnUnroll = NKV_ATTN_UNROLL;
-constexpr int kMaxQHeads = 32;  // the waves' LDS merge buffer: 4 KiB per query head
+constexpr int kMaxQHeads = 16;  // the waves' LDS merge buffer: 4 KiB per query head
 constexpr int kEntryRows = NKV_ATTN_ENTRY_ROWS;
 constexpr int kMaxEntryBlocks = 64;  // blocks one entry may span
 constexpr int kPlanThreads = 1024;
@@ -209,6 +213,27 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(
   }
 }
 
+// Stores one (entry, query head) partial: the wave's lanes hold dims
+// 2 lane, 2 lane + 1 of the unnormalised output (a0, a1) against reference
+// max mm with weight sum lsum.  The sums go out as fp16 pairs scaled by
+// 2^-k, k putting the largest magnitude in [2^14, 2^15); (mm + k, lsum 2^-k)
+// carries the same factor, so the merge stays exact.
+__device__ __forceinline__ void emit_partial(uint32_t* acc_out, f32x2* ml_out, float a0, float a1,
+                                             float mm, float lsum, int lane) {
+  float amax = fmaxf(fabsf(a0), fabsf(a1));
+#pragma unroll
+  for (int x = kWave / 2; x > 0; x >>= 1) amax = fmaxf(amax, __shfl_xor(amax, x, kWave));
+  const int e = static_cast<int>((__float_as_uint(amax) >> 23) & 0xFFu) - 127;
+  const int k = amax > 0.f ? min(112, max(-112, e - 14)) : 0;
+  const float down = __uint_as_float(static_cast<uint32_t>(127 - k) << 23);
+  const uint32_t packed =
+      static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a0 * down))) |
+      (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a1 * down)))
+       << 16);
+  store_stream(acc_out + lane, packed);
+  if (lane == 0) store_stream(ml_out, f32x2{mm + static_cast<float>(k), lsum * down});
+}
+
 // Shared state of one workgroup: the entry's cache rows, each wave's
 // partials, and the count of waves that have published theirs.
 template <int HQ>
@@ -234,9 +259,7 @@ struct AttnShared {
 // bumps an arrival counter; the last wave to arrive merges and stores them,
 // the others exit at once, so their slots go to the next workgroup instead
 // of idling until the slowest wave's loads return.
-// kRowHeads: kv heads in a cache row (HKV unless the layout is run in parts
-// of HKV heads).
-template <int HKV, int G, bool kHalf, int kRowHeads = HKV>
+template <int HKV, int G, bool kHalf>
 __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_seq_stride,
     const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
@@ -246,8 +269,8 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
   constexpr int HQ = HKV * G;
   constexpr int NC = HKV >= 4 ? HKV / 4 : 1;   // kv heads per lane per row
   constexpr int TPI = HKV >= 4 ? 1 : 4 / HKV;  // rows per wavefront load
-  constexpr int kRowBytes = kRowHeads * kHeadBytes;
-  static_assert(HQ <= kMaxQHeads && NC * G <= 8, "unsupported head layout");
+  constexpr int kRowBytes = HKV * kHeadBytes;
+  static_assert(HQ <= kMaxQHeads && NC * G <= 4, "unsupported head layout");
   __shared__ AttnShared<HQ> sh;
 
   const int64_t part = blockIdx.x;
@@ -452,20 +475,316 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
         lsum = fmaf(sh.l[w][qh], f, lsum);
       }
     }
-    float amax = fmaxf(fabsf(a0), fabsf(a1));
-#pragma unroll
-    for (int x = kWave / 2; x > 0; x >>= 1) amax = fmaxf(amax, __shfl_xor(amax, x, kWave));
-    const int e = static_cast<int>((__float_as_uint(amax) >> 23) & 0xFFu) - 127;
-    const int k = amax > 0.f ? min(112, max(-112, e - 14)) : 0;
-    const float down = __uint_as_float(static_cast<uint32_t>(127 - k) << 23);
-    const uint32_t packed =
-        static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a0 * down))) |
-        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(a1 * down)))
-         << 16);
-    store_stream(part_acc + (part * HQ + qh) * (kHeadDim / 2) + lane, packed);
-    if (lane == 0) {
-      store_stream(part_ml + part * HQ + qh, f32x2{mm + static_cast<float>(k), lsum * down});
+    emit_partial(part_acc + (part * HQ + qh) * (kHeadDim / 2), part_ml + part * HQ + qh, a0, a1,
+                 mm, lsum, lane);
+  }
+}
+
+// Grouped-query decode on MFMA.  With G = Hq / Hkv query heads per kv head
+// the VALU kernel above spends 2 G FLOPs per cache byte on v_dot2 and fma
+// (plus a DPP row sum per head), which outruns the memory time from G = 4
+// on.  Here the G query heads of one kv head form the 16 columns of one
+// MFMA tile (up to 16 heads, padding columns zero), so the arithmetic of a
+// 16-key chunk is a fixed 13 MFMAs whatever G is:
+//   * S^T = K Q^T: 4 x 16x16x32 (keys x heads, over 128 dims); a lane holds
+//     head c16 and keys 4 g4 + i, which is exactly the B layout of a
+//     16x16x16 MFMA over those keys, so P^T needs no shuffle;
+//   * O^T += V^T P^T: 8 x 16x16x16 (dims x heads, over 16 keys), V^T from
+//     the transposing LDS read; a ninth product against a row of ones sums
+//     the same (rounded) weights;
+//   * the online softmax is a 4-lane max per head and one exp2 per score.
+// A workgroup owns one (plan entry, kv head).  Its wavefronts take the
+// entry's 16-key chunks round-robin and run independently: each has a
+// private ring of kDecSlots chunk buffers in LDS, filled by global_load_lds
+// kDecSlots - 1 chunks ahead of the one it computes and waited for with a
+// counted s_waitcnt (8 copies per chunk), so no barrier sits in the loop.
+// The waves then merge through LDS (the last to arrive stores the entry's
+// partials, as above), in the same format, for the same reduce kernel.
+// Invalid rows (block id missing or outside the cache, keys past the entry)
+// copy cache row 0 into their slots; their scores are masked and their V
+// rows zeroed before the product.
+#ifndef NKV_DEC_WAVES
+#define NKV_DEC_WAVES 4  // wavefronts per workgroup
+#endif
+#ifndef NKV_DEC_SLOTS
+#define NKV_DEC_SLOTS 2  // 16-key chunk buffers per wavefront
+#endif
+#ifndef NKV_DEC_NT_LOADS
+#define NKV_DEC_NT_LOADS 1  // stream K/V past the caches (nt)
+#endif
+constexpr int kDecWaves = NKV_DEC_WAVES;
+constexpr int kDecThreads = kDecWaves * kWave;
+constexpr int kDecSlots = NKV_DEC_SLOTS;
+constexpr int kDecKeys = 16;                  // keys per chunk
+constexpr int kDecChunkWords = kDecKeys * 16;  // 16-byte words per K or V chunk
+constexpr int kDecCopies = 2 * kDecKeys / 4;   // copy instructions per chunk (K and V)
+constexpr int kDecMaxGroup = 16;               // query heads per kv head (MFMA columns)
+#ifndef NKV_DEC_MFMA_MIN_GROUP
+#define NKV_DEC_MFMA_MIN_GROUP 3  // smallest G run on MFMA (smaller G: the VALU kernel)
+#endif
+constexpr int kDecMfmaMinGroup = NKV_DEC_MFMA_MIN_GROUP;
+static_assert(kDecWaves == 2 || kDecWaves == 4 || kDecWaves == 8,
+              "NKV_DEC_WAVES must be 2, 4 or 8");
+static_assert(kDecSlots >= 2 && kDecSlots <= 4, "NKV_DEC_SLOTS must be in [2, 4]");
+
+// One wavefront's LDS: its ring while it runs, its partials afterwards.
+union DecWaveMem {
+  struct {
+    u32x4 k[kDecSlots][kDecChunkWords];
+    u32x4 v[kDecSlots][kDecChunkWords];
+  } ring;
+  struct {
+    float acc[kDecMaxGroup][kHeadDim];
+    float m[kDecMaxGroup];
+    float l[kDecMaxGroup];
+  } part;
+};
+struct DecShared {
+  DecWaveMem wave[kDecWaves];
+  int32_t rows[(kEntryRows + kDecKeys - 1) / kDecKeys * kDecKeys];  // whole chunks
+  uint32_t arrived;
+};
+
+// s_waitcnt vmcnt(n) with the other counters left alone, and a compiler
+// barrier for memory (the LDS reads after it must stay after it).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+template <bool kWide, bool kHalf>
+__global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
+    const uint16_t* __restrict__ q, int64_t q_seq_stride,
+    const uint8_t* __restrict__ key_cache, const uint8_t* __restrict__ value_cache,
+    const int32_t* __restrict__ tables, int64_t table_stride, int32_t block_size,
+    int32_t num_blocks, int32_t num_kv_heads, int32_t group, const int4* __restrict__ plan,
+    int32_t num_seqs, float scale_log2, uint32_t* __restrict__ part_acc,
+    f32x2* __restrict__ part_ml) {
+  typedef Elem<kHalf> E;
+  typedef typename E::T T;
+  typedef typename E::X8 X8;
+  typedef typename E::X4 X4;
+  __shared__ DecShared sh;
+
+  const int64_t part = blockIdx.x / num_kv_heads;
+  const int32_t kh = static_cast<int32_t>(blockIdx.x % num_kv_heads);
+  const int4 entry = plan[part];
+  const int32_t row0 = entry.x;
+  const int32_t seq = entry.z;
+  // Uniform exits for entries outside every sequence; an empty cache
+  // (num_blocks == 0) has no row to read, and its entries store (-inf, 0).
+  if (entry.y <= 0 || seq < 0 || seq >= num_seqs || row0 < 0) return;
+  const int32_t nrows = num_blocks > 0 ? min(entry.y, kEntryRows) : 0;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
+
+  for (int32_t t = tid; t < nrows; t += kDecThreads) {
+    const int32_t ctx = row0 + t;
+    const int32_t logical = ctx / block_size;
+    int32_t cache_row = -1;
+    if (logical < table_stride) {
+      const int32_t block = tables[static_cast<int64_t>(seq) * table_stride + logical];
+      if (block >= 0 && block < num_blocks) cache_row = block * block_size + ctx % block_size;
     }
+    sh.rows[t] = cache_row;
+  }
+  if (tid == 0) sh.arrived = 0u;
+
+  // Q^T operands (B of S^T = K Q^T): lane holds head c16 of this kv head,
+  // dims 32 dc + 8 g4 .. +8; zero for padding columns.
+  X8 qb[4];
+  {
+    const bool col_ok = c16 < group;
+    const uint16_t* qrow = q + static_cast<int64_t>(seq) * q_seq_stride +
+                           static_cast<int64_t>(kh * group + (col_ok ? c16 : 0)) * kHeadDim;
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (col_ok) v = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * g4);
+      qb[dc] = __builtin_bit_cast(X8, v);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // q and the block ids have landed (nothing else in flight)
+  __syncthreads();                // rows resolved, counter zero
+
+  const uint32_t row_bytes = static_cast<uint32_t>(num_kv_heads) * kHeadBytes;
+  const uint8_t* const k_head = key_cache + static_cast<int64_t>(kh) * kHeadBytes;
+  const uint8_t* const v_head = value_cache + static_cast<int64_t>(kh) * kHeadBytes;
+  DecWaveMem& mine = sh.wave[wave];
+  // LDS byte addresses of this wave's ring (uniform; the copies' M0 base).
+  const uint32_t ring_k = lds_address(&sh.wave[0].ring.k[0][0]) +
+                          static_cast<uint32_t>(wave) * sizeof(DecWaveMem);
+  const uint32_t ring_v = ring_k + kDecSlots * kDecChunkWords * 16;
+
+  const int32_t nchunks = (nrows + kDecKeys - 1) / kDecKeys;
+  const int32_t count = wave < nchunks ? (nchunks - wave + kDecWaves - 1) / kDecWaves : 0;
+
+  // Copies of the wave's chunk j (entry keys 16 (wave + waves j) ..) into
+  // slot j % kDecSlots: instruction i moves keys 4 i .. 4 i + 3, lane l the
+  // 16-byte chunk that the swizzle puts at position l % 16 of key 4 i + l / 16.
+  auto issue = [&](int32_t j) {
+    const int32_t key0 = (wave + kDecWaves * j) * kDecKeys;
+    const uint32_t slot_off = static_cast<uint32_t>(j % kDecSlots) * kDecChunkWords * 16;
+    int32_t row[kDecKeys / 4];
+#pragma unroll
+    for (int i = 0; i < kDecKeys / 4; ++i) {
+      const int32_t t = key0 + 4 * i + g4;
+      const int32_t r = t < nrows ? sh.rows[t] : -1;
+      row[i] = r >= 0 ? r : 0;  // invalid: an in-bounds row, masked and zeroed later
+    }
+#pragma unroll
+    for (int i = 0; i < kDecKeys / 4; ++i) {
+      const int key = 4 * i + g4;
+      const uint32_t kc = 16u * static_cast<uint32_t>(c16 ^ (key & 15));
+      const uint32_t vc = 16u * static_cast<uint32_t>(c16 ^ ((key & 7) << 1));
+      const uint32_t dst = slot_off + static_cast<uint32_t>(4 * i) * 256u;
+      constexpr bool kNt = NKV_DEC_NT_LOADS != 0;
+      if (kWide) {
+        const int64_t base = static_cast<int64_t>(row[i]) * row_bytes;
+        lds_copy16<kNt>(k_head + base + kc, ring_k + dst);
+        lds_copy16<kNt>(v_head + base + vc, ring_v + dst);
+      } else {
+        const uint32_t base = static_cast<uint32_t>(row[i]) * row_bytes;
+        lds_copy16<kNt>(k_head, base + kc, ring_k + dst);
+        lds_copy16<kNt>(v_head, base + vc, ring_v + dst);
+      }
+    }
+  };
+
+  float row_max = -INFINITY;  // reference max of head c16 (log2 units)
+  // O^T blocks: dims 16 db + 4 g4 + i of head c16; block 8 is the ones
+  // product, whose g4 == 0, i == 0 entry is the head's weight sum.
+  f32x4 acc[9];
+#pragma unroll
+  for (int db = 0; db < 9; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const T one = c16 == 0 ? static_cast<T>(1.f) : static_cast<T>(0.f);
+  const X4 ones = {one, one, one, one};
+  const int tr_key = 4 * g4 + ((lane >> 2) & 3);  // key this lane addresses in a V^T read
+  const int tr_dim = 4 * (lane & 3);              // first dim it addresses, within 16
+
+#pragma unroll
+  for (int32_t j = 0; j < kDecSlots - 1; ++j) {
+    if (j < count) issue(j);
+  }
+  for (int32_t j = 0; j < count; ++j) {
+    const int32_t ahead = j + kDecSlots - 1;
+    if (ahead < count) {
+      // The slot receiving chunk `ahead` was read by the previous chunk's
+      // products; their LDS reads are complete before it is overwritten.
+      asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+      issue(ahead);
+    }
+    // Chunks issued after j: min(kDecSlots - 1, count - 1 - j), 8 copies each.
+    const int32_t later = min(kDecSlots - 1, count - 1 - j);
+    if (later >= 3) {
+      wait_vmcnt<3 * kDecCopies>();
+    } else if (later == 2) {
+      wait_vmcnt<2 * kDecCopies>();
+    } else if (later == 1) {
+      wait_vmcnt<kDecCopies>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    const int slot = j % kDecSlots;
+    const u32x4* const k_tile = mine.ring.k[slot];
+    u32x4* const v_tile = mine.ring.v[slot];
+    const int32_t key0 = (wave + kDecWaves * j) * kDecKeys;
+
+    // Keys of this lane's scores (4 g4 + i) and whether each is valid.
+    bool bad[4];
+    {
+      const int32_t t = key0 + 4 * g4;
+      const int4 r = *reinterpret_cast<const int4*>(&sh.rows[t]);  // t % 4 == 0, whole chunks
+      const int32_t rr[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bad[i] = t + i >= nrows || rr[i] < 0;
+    }
+    const bool any_bad = __any(bad[0] || bad[1] || bad[2] || bad[3]);
+    if (any_bad) {  // zero V of invalid keys: lane covers key 4 i + g4, chunk c16
+#pragma unroll
+      for (int i = 0; i < kDecKeys / 4; ++i) {
+        const int32_t t = key0 + 4 * i + g4;
+        if (t >= nrows || sh.rows[t] < 0) v_tile[(4 * i + g4) * 16 + c16] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) {
+      const X8 a = __builtin_bit_cast(X8, k_tile[k_index(c16, 4 * dc + g4)]);
+      s = E::mfma(a, qb[dc], s);
+    }
+    if (any_bad) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] = bad[i] ? -INFINITY : s[i];
+    }
+    float local = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    local = row4_max(local) * scale_log2;  // scale > 0: the max commutes with it
+    const bool move = local > row_max + kRescaleLog2;
+    if (__any(move)) {
+      const float m_new = move ? local : row_max;
+      const float alpha = move ? exp2_fast(row_max - m_new) : 1.f;  // 0 from -inf
+#pragma unroll
+      for (int db = 0; db < 9; ++db) acc[db] *= alpha;
+      row_max = m_new;
+    }
+    const float ref = row_max == -INFINITY ? INFINITY : row_max;  // nothing valid yet: weights 0
+    X4 pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pb[i] = static_cast<T>(exp2_fast(__builtin_fmaf(s[i], scale_log2, -ref)));
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const X4 a = __builtin_bit_cast(X4, v_tr_read(v_tile, tr_key, 16 * db + tr_dim));
+      acc[db] = E::mfma16(a, pb, acc[db]);
+    }
+    acc[8] = E::mfma16(ones, pb, acc[8]);
+  }
+
+  // Publish this wave's partials in its own (drained) ring.
+  if (c16 < group) {
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      *reinterpret_cast<f32x4*>(&mine.part.acc[c16][16 * db + 4 * g4]) = acc[db];
+    }
+    if (g4 == 0) {
+      mine.part.m[c16] = row_max;
+      mine.part.l[c16] = acc[8][0];
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  uint32_t before = 0u;
+  if (lane == 0) {
+    before = __hip_atomic_fetch_add(&sh.arrived, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  before = __builtin_amdgcn_readfirstlane(before);
+  if (before != kDecWaves - 1) return;  // whole wavefront; no barrier follows
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+  const int64_t num_q_heads = static_cast<int64_t>(num_kv_heads) * group;
+  for (int g = 0; g < group; ++g) {
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) mm = fmaxf(mm, sh.wave[w].part.m[g]);
+    float a0 = 0.f, a1 = 0.f, lsum = 0.f;
+    if (mm != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const float mw = sh.wave[w].part.m[g];
+        const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - mm);
+        a0 = fmaf(sh.wave[w].part.acc[g][2 * lane], f, a0);
+        a1 = fmaf(sh.wave[w].part.acc[g][2 * lane + 1], f, a1);
+        lsum = fmaf(sh.wave[w].part.l[g], f, lsum);
+      }
+    }
+    const int64_t qh = static_cast<int64_t>(kh) * group + g;
+    emit_partial(part_acc + (part * num_q_heads + qh) * (kHeadDim / 2),
+                 part_ml + part * num_q_heads + qh, a0, a1, mm, lsum, lane);
   }
 }
 
@@ -542,50 +861,26 @@ template <bool kHalf>
 PartialKernel partial_kernel_for(int64_t hkv, int64_t g) {
 #define NKV_ATTN_CASE(H, GG) \
   if (hkv == H && g == GG) return attn_decode_partial_kernel<H, GG, kHalf>;
-  // Every layout with G <= 8 query heads per kv head (G <= 4 with 8 kv
-  // heads: a lane keeps 2 kv heads x G query heads in registers).
+  // One or two query heads per kv head; more go to the MFMA kernel.
   NKV_ATTN_CASE(8, 1)
   NKV_ATTN_CASE(8, 2)
-  NKV_ATTN_CASE(8, 3)
-  NKV_ATTN_CASE(8, 4)
   NKV_ATTN_CASE(4, 1)
   NKV_ATTN_CASE(4, 2)
-  NKV_ATTN_CASE(4, 3)
-  NKV_ATTN_CASE(4, 4)
-  NKV_ATTN_CASE(4, 5)
-  NKV_ATTN_CASE(4, 6)
-  NKV_ATTN_CASE(4, 7)
-  NKV_ATTN_CASE(4, 8)
   NKV_ATTN_CASE(2, 1)
   NKV_ATTN_CASE(2, 2)
-  NKV_ATTN_CASE(2, 3)
-  NKV_ATTN_CASE(2, 4)
-  NKV_ATTN_CASE(2, 5)
-  NKV_ATTN_CASE(2, 6)
-  NKV_ATTN_CASE(2, 7)
-  NKV_ATTN_CASE(2, 8)
   NKV_ATTN_CASE(1, 1)
   NKV_ATTN_CASE(1, 2)
-  NKV_ATTN_CASE(1, 3)
-  NKV_ATTN_CASE(1, 4)
-  NKV_ATTN_CASE(1, 5)
-  NKV_ATTN_CASE(1, 6)
-  NKV_ATTN_CASE(1, 7)
-  NKV_ATTN_CASE(1, 8)
 #undef NKV_ATTN_CASE
   return nullptr;
 }
-// 8 kv heads with 5 to 8 query heads each (40 to 64 query heads): run as
-// two parts of 4 kv heads, each reading its half of every cache row.
-template <bool kHalf>
-PartialKernel split_partial_kernel_for(int64_t g) {
-  switch (g) {
-    case 5: return attn_decode_partial_kernel<4, 5, kHalf, 8>;
-    case 6: return attn_decode_partial_kernel<4, 6, kHalf, 8>;
-    case 7: return attn_decode_partial_kernel<4, 7, kHalf, 8>;
-    case 8: return attn_decode_partial_kernel<4, 8, kHalf, 8>;
-    default: return nullptr;
-  }
+
+using DecodeMfmaKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const uint8_t*,
+                                   const int32_t*, int64_t, int32_t, int32_t, int32_t, int32_t,
+                                   const int4*, int32_t, float, uint32_t*, f32x2*);
+
+DecodeMfmaKernel mfma_kernel_for(bool wide, bool half) {
+  if (wide) return half ? attn_decode_mfma_kernel<true, true> : attn_decode_mfma_kernel<true, false>;
+  return half ? attn_decode_mfma_kernel<false, true> : attn_decode_mfma_kernel<false, false>;
 }
 
 }  // namespace
@@ -657,18 +952,21 @@ extern "C" int nkv_paged_attention_decode(
                     "nkv_paged_attention_decode: num_q_heads must be a multiple of num_kv_heads");
   }
   const int64_t group = num_q_heads / num_kv_heads;
-  PartialKernel kernel = half ? partial_kernel_for<true>(num_kv_heads, group)
-                              : partial_kernel_for<false>(num_kv_heads, group);
-  int64_t parts = 1;  // launches, each over num_kv_heads / parts kv heads
-  if (kernel == nullptr && num_kv_heads == 8) {
-    kernel = half ? split_partial_kernel_for<true>(group) : split_partial_kernel_for<false>(group);
-    parts = 2;
+  // MFMA from kDecMfmaMinGroup query heads per kv head on, and for every
+  // layout the VALU kernels do not cover; the VALU kernel below that.
+  bool use_mfma = group >= kDecMfmaMinGroup && group <= kDecMaxGroup;
+  PartialKernel kernel = nullptr;
+  if (!use_mfma) {
+    kernel = half ? partial_kernel_for<true>(num_kv_heads, group)
+                  : partial_kernel_for<false>(num_kv_heads, group);
+    if (kernel == nullptr && group <= kDecMaxGroup) use_mfma = true;
   }
-  if (kernel == nullptr) {
+  if (!use_mfma && kernel == nullptr) {
     return nkv_fail(NKV_E_INVALID,
                     "nkv_paged_attention_decode: unsupported head layout %lld kv x %lld q "
-                    "(kv heads 1/2/4/8, at most 8 query heads per kv head)",
-                    static_cast<long long>(num_kv_heads), static_cast<long long>(num_q_heads));
+                    "(at most %d query heads per kv head)",
+                    static_cast<long long>(num_kv_heads), static_cast<long long>(num_q_heads),
+                    kDecMaxGroup);
   }
   if (num_seqs < 0 || num_seqs > NKV_MAX_PLAN_SEQS || capacity < 0 || capacity > INT32_MAX ||
       block_size <= 0 || num_blocks < 0 || num_blocks * block_size > INT32_MAX ||
@@ -700,37 +998,41 @@ extern "C" int nkv_paged_attention_decode(
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float scale_log2 = scale * 1.4426950408889634f;  // log2(e)
-  // Each part covers num_kv_heads / parts kv heads and their query heads:
-  // q, out and the caches advance by that many heads; the parts run one
-  // after the other on the stream and share the workspace.
-  const int64_t part_q_heads = num_q_heads / parts;
-  auto* part_acc = static_cast<uint32_t*>(workspace);  // fp16 pairs
-  auto* part_ml = reinterpret_cast<f32x2*>(part_acc + capacity * part_q_heads * head_dim / 2);
-  for (int64_t p = 0; p < parts; ++p) {
-    const int64_t q_off = p * part_q_heads * head_dim;                        // elements
-    const int64_t kv_off = p * (num_kv_heads / parts) * head_dim * 2;         // bytes
-    if (capacity > 0) {
-      kernel<<<dim3(static_cast<unsigned>(capacity)), dim3(kAttnThreads), 0, s>>>(
-          static_cast<const uint16_t*>(q) + q_off, q_seq_stride,
-          static_cast<const uint8_t*>(key_cache) + kv_off,
-          static_cast<const uint8_t*>(value_cache) + kv_off, block_tables, table_stride,
-          static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
-          static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2, part_acc,
-          part_ml);
-      if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
-    }
-    const dim3 reduce_grid(static_cast<unsigned>(num_seqs), static_cast<unsigned>(part_q_heads));
-    uint16_t* part_out = static_cast<uint16_t*>(out) + q_off;
-    if (half) {
-      attn_decode_reduce_kernel<true><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-          part_acc, part_ml, first_part, capacity, static_cast<int32_t>(part_q_heads), part_out,
-          out_seq_stride);
-    } else {
-      attn_decode_reduce_kernel<false><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-          part_acc, part_ml, first_part, capacity, static_cast<int32_t>(part_q_heads), part_out,
-          out_seq_stride);
-    }
-    if (int rc = nkv_check_launch("nkv_paged_attention_decode (reduce)")) return rc;
+  if (use_mfma && (capacity * num_kv_heads > INT32_MAX || num_kv_heads * head_dim * 2 > INT32_MAX)) {
+    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: plan too long for the grid");
   }
-  return NKV_OK;
+  auto* part_acc = static_cast<uint32_t*>(workspace);  // fp16 pairs
+  auto* part_ml = reinterpret_cast<f32x2*>(part_acc + capacity * num_q_heads * head_dim / 2);
+  if (capacity > 0 && use_mfma) {
+    // byte offsets into a cache past 4 GiB need 64-bit addresses
+    const bool wide = num_blocks * block_size * num_kv_heads * head_dim * 2 > UINT32_MAX;
+    mfma_kernel_for(wide, half)<<<dim3(static_cast<unsigned>(capacity * num_kv_heads)),
+                                  dim3(kDecThreads), 0, s>>>(
+        static_cast<const uint16_t*>(q), q_seq_stride, static_cast<const uint8_t*>(key_cache),
+        static_cast<const uint8_t*>(value_cache), block_tables, table_stride,
+        static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
+        static_cast<int32_t>(num_kv_heads), static_cast<int32_t>(group),
+        static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2, part_acc,
+        part_ml);
+    if (int rc = nkv_check_launch("nkv_paged_attention_decode (MFMA partials)")) return rc;
+  } else if (capacity > 0) {
+    kernel<<<dim3(static_cast<unsigned>(capacity)), dim3(kAttnThreads), 0, s>>>(
+        static_cast<const uint16_t*>(q), q_seq_stride, static_cast<const uint8_t*>(key_cache),
+        static_cast<const uint8_t*>(value_cache), block_tables, table_stride,
+        static_cast<int32_t>(block_size), static_cast<int32_t>(num_blocks),
+        static_cast<const int4*>(plan), static_cast<int32_t>(num_seqs), scale_log2, part_acc,
+        part_ml);
+    if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
+  }
+  const dim3 reduce_grid(static_cast<unsigned>(num_seqs), static_cast<unsigned>(num_q_heads));
+  if (half) {
+    attn_decode_reduce_kernel<true><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
+        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
+        static_cast<uint16_t*>(out), out_seq_stride);
+  } else {
+    attn_decode_reduce_kernel<false><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
+        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
+        static_cast<uint16_t*>(out), out_seq_stride);
+  }
+  return nkv_check_launch("nkv_paged_attention_decode (reduce)");
 }

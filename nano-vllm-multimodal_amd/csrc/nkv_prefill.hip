@@ -34,6 +34,7 @@
 #include <type_traits>
 
 #include "nkv_common.h"
+#include "nkv_mfma.h"
 
 namespace nkv {
 namespace {
@@ -55,70 +56,14 @@ constexpr int kPfPlanThreads = 1024;
 // division, far from fp32 / bf16 / fp16 overflow.
 constexpr float kRescaleLog2 = 8.f;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
 // K and V tiles, double-buffered, copied straight from global memory into
 // LDS by global_load_lds (one wavefront instruction fills 1 KiB of
 // consecutive LDS: 4 keys x 256 B; the source address of each lane picks
-// the chunk that belongs at its position).  Both are [key][16-byte chunk],
-// the chunks of key r swizzled so that the MFMA operand reads are
-// conflict-free:
-//   K: chunk c at c ^ (r % 16)    (ds_read_b128: 16 keys at one chunk)
-//   V: chunk c at c ^ 2 (r % 8)   (ds_read_b64_tr_b16: 16 keys x 32 bytes)
-// Each buffer is its own __shared__ array, and the loop body is compiled
-// once per buffer parity, so the compiler can tell the tile being read from
-// the one being copied into and does not wait for the copies in flight.
+// the chunk that belongs at its position), in the swizzled layout of
+// k_index / v_index.  Each buffer is its own __shared__ array, and the loop
+// body is compiled once per buffer parity, so the compiler can tell the tile
+// being read from the one being copied into.
 constexpr int kTileChunks = kPfKeys * 16;  // 16-byte chunks per K or V tile
-
-__device__ __forceinline__ int k_index(int key, int chunk) {
-  return key * 16 + (chunk ^ (key & 15));
-}
-__device__ __forceinline__ int v_index(int key, int chunk) {
-  return key * 16 + (chunk ^ ((key & 7) << 1));
-}
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-
-// The element type: bf16 (kHalf false) or fp16 (kHalf true), with its 8-
-// and 4-wide vectors and the matching MFMA.
-template <bool kHalf>
-struct Elem {
-  typedef __bf16 T;
-  typedef bf16x8 X8;
-  typedef bf16x4 X4;
-  static __device__ __forceinline__ f32x4 mfma(X8 a, X8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Elem<true> {
-  typedef _Float16 T;
-  typedef f16x8 X8;
-  typedef f16x4 X4;
-  static __device__ __forceinline__ f32x4 mfma(X8 a, X8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-
-// Max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row's
-// lanes), with the cross-row swaps of gfx950 (no LDS traffic).
-__device__ __forceinline__ float row4_max(float x) {
-  auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-  p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-}
-__device__ __forceinline__ float row4_sum(float x) {
-  auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-  p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
 
 // Plan: one int4 {seq, token0, tokens, 0} per workgroup: tokens [token0,
 // token0 + tokens) of sequence seq's queries, tokens <= tile_tokens.
@@ -238,32 +183,6 @@ __device__ __forceinline__ void resolve_rows(int32_t* rows, int32_t* invalid, co
   if (lane == 0) *invalid = any_invalid ? 1 : 0;
 }
 
-// One wavefront copies 16 bytes per lane from global memory straight into
-// LDS: lane l's bytes land at lds_dst + 16 l (global_load_lds_dwordx4, LDS
-// base in M0).  Written as asm so that the compiler, which cannot tell which
-// LDS buffer such a copy writes, does not make every later LDS access wait
-// for it: the kernel waits for its copies itself (s_waitcnt, then a barrier)
-// before it reads the buffer they fill.
-// LDS byte address of a __shared__ array (a constant once inlined).
-__device__ __forceinline__ uint32_t lds_address(const u32x4* array) {
-  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_u32x4*)array));
-}
-// Source as a 64-bit per-lane address; lds_dst is wave-uniform.
-__device__ __forceinline__ void lds_copy16(const uint8_t* src, uint32_t lds_dst) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(src), "s"(lds_dst)
-               : "m0", "memory");
-}
-// Source as a wave-uniform base (SGPRs) plus a per-lane 32-bit byte offset.
-__device__ __forceinline__ void lds_copy16(const uint8_t* base, uint32_t offset, uint32_t lds_dst) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(offset), "s"(base), "s"(lds_dst)
-               : "m0", "memory");
-}
-
 // This wavefront's share of the copies of one K or V tile: 64 / waves
 // consecutive keys, 4 keys per instruction; lane l copies 16-byte chunk
 // swizzle(l % 16) of key l / 16.  The block rows are read first, so the
@@ -294,19 +213,6 @@ __device__ __forceinline__ void issue_copies(const u32x4* dst, const int32_t* ro
       }
     }
   }
-}
-
-// Four consecutive bf16 of V^T for the PV product: lane 16 G + 4 j + q
-// supplies the address of V[key][dim4 .. +4] and receives, as lane 16 G + i,
-// V[key of lane 16 G + 4 j'][dim of lane 16 G + i] for j' = 0..3 (the
-// gfx950 transposing LDS read).
-__device__ __forceinline__ u32x2 v_tr_read(const u32x4* v_tile, int key, int dim4) {
-  const int byte = (v_index(key, dim4 >> 3) << 4) + ((dim4 & 7) << 1);
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) char lds_char;
-  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-  lds_v4i16* p = (lds_v4i16*)((lds_char*)(v_tile) + byte);  // generic -> LDS
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p));
 }
 
 // Workgroups are handed to the 8 XCDs round-robin by linear id (id % 8), and

@@ -6,8 +6,9 @@ flash_attn_varlen_func, flash_attn_with_kvcache`` with an import from this
 module; the calls stay as they are.
 
 Only what the reference passes is supported: causal attention, bfloat16 or
-float16, head_dim 128, 1 to 8 query heads per kv head, no dropout, window,
-alibi or softcap.  Anything else raises instead of computing something
+float16, head_dim 128, 1 to 8 query heads per kv head for prefill (1, 2, 4
+or 8 kv heads) and 1 to 16 for decode, no dropout, window, alibi or
+softcap.  Anything else raises instead of computing something
 different.
 """
 from __future__ import annotations
