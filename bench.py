@@ -27,7 +27,10 @@ store, prefix-cache gather, narrow rows) kernel by kernel; "gpu_reference"
 runs the reference pytorch backend's torch ops on the same GPU, on the
 decode step and on the reference's own store/gather microbenchmark matrix;
 "prefill_attention" times the causal paged prefill kernel on the
-chunked-prefill step against the reference's SDPA prefill path.
+chunked-prefill step against the reference's SDPA prefill path;
+"grouped_decode_attention" times one decode-attention layer over the same
+contexts for the grouped-query layouts of Qwen2.5-VL-3B / -7B and
+Qwen3-VL-8B (the MFMA decode kernel).
 """
 from __future__ import annotations
 
@@ -254,6 +257,11 @@ def main(argv=None) -> int:
             f"{prefill_attention['us']:.1f} us, {prefill_attention['tflops']:.0f} TFLOP/s, "
             f"torch SDPA path {prefill_attention['torch_sdpa_path_us']:.0f} us")
 
+    grouped_decode = measure_grouped_decode(device, backend, wl, args.steps)
+    for rec in grouped_decode:
+        log(f"[bench] decode attention {rec['layout']}: {rec['us']:.1f} us, "
+            f"{rec['achieved']:.0f} GB/s ({rec['kernel']})")
+
     gpu_reference = None
     if args.gpu_reference and not args.profile:
         gpu_reference = {
@@ -375,6 +383,7 @@ def main(argv=None) -> int:
         "copy_reference": copy_reference,
         "other_workloads": other_workloads,
         "prefill_attention": prefill_attention,
+        "grouped_decode_attention": grouped_decode,
         "gpu_reference": gpu_reference,
         "block_pool": block_pool,
         "cpu_baseline": cpu_baseline,
@@ -386,6 +395,74 @@ def main(argv=None) -> int:
 
 
 MI355X_BF16_DENSE_TFLOPS = 2500.0
+
+# Grouped-query layouts of the Qwen vision-language families: (name, kv heads,
+# query heads per kv head).  16 over 8 is the decode step's own layout.
+GROUPED_LAYOUTS = (
+    ("Qwen2.5-VL-3B: 16 q / 2 kv heads", 2, 8),
+    ("Qwen2.5-VL-7B: 28 q / 4 kv heads", 4, 7),
+    ("Qwen3-VL-8B: 32 q / 8 kv heads", 8, 4),
+)
+
+
+def measure_grouped_decode(device, backend, wl, reps: int) -> list[dict]:
+    """Paged-attention decode of one layer over the decode step's 256
+    contexts (block 256, blocks placed at random) for the grouped-query
+    layouts above: G = 7 and 8 run on the MFMA kernel, as does G = 4.  One
+    event pair on the current stream around `reps` calls (partials + merge);
+    bytes = the K and V rows read once, plus q and out."""
+    import numpy as np
+    import torch
+
+    from nanokv.benchmark import MI355X_HBM_PEAK_GBPS
+
+    lens = np.asarray(wl.num_tokens, dtype=np.int64)
+    bs = wl.block_size
+    need = -(-lens // bs)
+    nb = int(need.sum()) + 8
+    total = int(lens.sum())
+    gen = torch.Generator(device=device).manual_seed(29)
+    perm = torch.randperm(nb, device=device, generator=gen).to(torch.int32)
+    tables = torch.full((lens.size, int(need.max())), -1, dtype=torch.int32, device=device)
+    cursor = 0
+    for i, n in enumerate(need.tolist()):
+        tables[i, :n] = perm[cursor:cursor + n]
+        cursor += n
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=device)
+    records = []
+    for name, hkv, g in GROUPED_LAYOUTS:
+        kc = torch.empty((nb, bs, hkv, 128), dtype=torch.bfloat16, device=device)
+        kc.normal_(generator=gen)
+        vc = torch.empty_like(kc).normal_(generator=gen)
+        q = torch.randn((lens.size, hkv * g, 128), device=device, generator=gen).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        plan = backend.build_attention_plan(kc, cu, total)
+        scale = 1.0 / math.sqrt(128)
+
+        def call():
+            backend.paged_attention_decode(q, kc, vc, tables, cu, total, scale, plan=plan, out=out)
+
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            call()
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / reps
+        nbytes = total * hkv * 128 * 2 * 2 + 2 * q.numel() * 2
+        achieved = nbytes / (us * 1e-6) / 1e9
+        records.append({
+            "layout": name, "kv_heads": hkv, "q_heads_per_kv_head": g,
+            "kernel": "attn_decode_mfma_kernel" if g >= 3 else "attn_decode_partial_kernel",
+            "us": round(us, 2), "algorithmic_bytes": nbytes, "achieved": round(achieved, 1),
+            "unit": "GB/s", "frac": round(achieved / MI355X_HBM_PEAK_GBPS, 4),
+        })
+        del kc, vc
+        torch.cuda.empty_cache()
+    return records
 
 
 def chunked_prefill_shape(seed: int = 17):
