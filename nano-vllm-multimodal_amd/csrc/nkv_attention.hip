@@ -339,7 +339,7 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
       const int32_t cache_row = t < nrows ? sh.rows[t] : -1;
       ok[u] = cache_row >= 0;
       // A skipped row re-reads cache row 0 (in bounds: the cache is not
-      // empty here) and gets a -inf score, i.e. zero weight.
+      // empty here), gets a -inf score and zeroed V words.
       const int64_t safe_row = ok[u] ? cache_row : 0;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -352,6 +352,21 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
         kw[u][c] = *reinterpret_cast<const u32x4*>(key_cache + off);
         vw[u][c] = *reinterpret_cast<const u32x4*>(value_cache + off);
 #endif
+      }
+    }
+    // A skipped row's bytes may be any bits (row 0 need not hold a written
+    // row): its score is -inf below, and its V words are zeroed here, since
+    // a zero weight times NaN or Inf would still reach the sums.
+    bool group_ok = true;
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) group_ok = group_ok && ok[u];
+    if (!__all(group_ok)) {
+#pragma unroll
+      for (int u = 0; u < kAttnUnroll; ++u) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          if (!ok[u]) vw[u][c] = u32x4{0u, 0u, 0u, 0u};
+        }
       }
     }
     float s[kAttnUnroll][NC][G];

@@ -204,6 +204,39 @@ def test_invalid_block_ids_drop_their_rows(backend, gpu_device, hkv, g):
     check_close(out, ref, "invalid blocks")
 
 
+@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 1), (1, 2), (2, 8), (4, 4)])
+def test_rows_outside_the_contexts_may_hold_any_bits(backend, gpu_device, hkv, g):
+    """Cache rows no context owns may hold any bits (a cache from torch.empty,
+    freed blocks): here NaN and +-Inf in block 0 (which no table uses), in
+    the spare blocks and in the unwritten tail of every context's last
+    block.  The kernels read such rows only as skipped rows, so the result
+    is the oracle's, finite, for the VALU kernel (G <= 2, including 2 and
+    4 rows per wavefront load) and the MFMA kernel."""
+    bs = 16
+    lens = [1, 5, bs, 3 * bs + 7, 40, 2, 0]
+    dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=hkv * 31 + g)
+    nan, inf = float("nan"), float("inf")
+    kc = torch.cat([torch.full_like(dev["kc"][:1], nan), dev["kc"]])
+    vc = torch.cat([torch.full_like(dev["vc"][:1], inf), dev["vc"]])
+    tables = torch.where(dev["tables"] >= 0, dev["tables"] + 1, dev["tables"])
+    for i, n in enumerate(lens):
+        if n == 0:
+            continue
+        last = int(host["tables"][i, (n - 1) // bs]) + 1
+        tail = n - (n - 1) // bs * bs
+        kc[last, tail:] = nan
+        vc[last, tail:] = -inf
+    used = set(host["tables"][host["tables"] >= 0].tolist())
+    for b in range(dev["kc"].shape[0]):
+        if b not in used:
+            kc[b + 1] = inf
+            vc[b + 1] = nan
+    scale = 1.0 / math.sqrt(128)
+    out = backend.paged_attention_decode(dev["q"], kc, vc, tables, dev["cu"], total, scale)
+    assert torch.isfinite(out).all(), "a skipped row reached the sums"
+    check_close(out, reference(host, scale), f"any-bits rows hkv={hkv} g={g}")
+
+
 @pytest.mark.parametrize("hq", [16, 32])
 def test_decode_step_layer_full_size(backend, gpu_device, hq):
     """One layer of the 256-sequence decode step (contexts log-uniform in
