@@ -276,6 +276,34 @@ def test_cache_over_4gib(backend, gpu_device):
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
+def test_rows_outside_the_contexts_may_hold_any_bits(backend, gpu_device, hkv, g):
+    """Cache rows no context owns may hold any bits: NaN and +-Inf in block 0
+    (which no table uses), in the spare blocks and in the unwritten tail of
+    every context's last block.  The result is the oracle's, finite."""
+    bs = 16
+    q_lens, k_lens = [5, 1, 40, 16], [5, 33, 70, 16]
+    dev, host = build_case(gpu_device, hkv, g, bs, q_lens, k_lens, seed=hkv * 17 + g)
+    nan, inf = float("nan"), float("inf")
+    kc = torch.cat([torch.full_like(dev["kc"][:1], nan), dev["kc"]])
+    vc = torch.cat([torch.full_like(dev["vc"][:1], -inf), dev["vc"]])
+    tables = torch.where(dev["tables"] >= 0, dev["tables"] + 1, dev["tables"])
+    for i, n in enumerate(k_lens):
+        last = int(host["tables"][i, (n - 1) // bs]) + 1
+        tail = n - (n - 1) // bs * bs
+        kc[last, tail:] = inf
+        vc[last, tail:] = nan
+    used = set(host["tables"][host["tables"] >= 0].tolist())
+    for b in range(dev["kc"].shape[0]):
+        if b not in used:
+            kc[b + 1] = nan
+            vc[b + 1] = inf
+    scale = 1.0 / math.sqrt(128)
+    out = backend.paged_attention_prefill(dev["q"], kc, vc, tables, dev["cu_q"], dev["cu_k"], scale)
+    assert torch.isfinite(out).all(), "a row outside the contexts reached the sums"
+    check_close(out, *reference(host, scale), f"any-bits rows hkv={hkv} g={g}")
+
+
 def test_unsupported_layouts_raise(backend, gpu_device):
     dev, _ = build_case(gpu_device, 3, 1, 16, [4], [4], seed=1)
     q9 = torch.zeros((4, 27, 128), dtype=torch.bfloat16, device=gpu_device)  # G = 9
