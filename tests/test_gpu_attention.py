@@ -112,12 +112,16 @@ def test_decode_attention_float16_matches_oracle(backend, gpu_device, hkv, g, bs
     check_close(out, ref, f"fp16 hkv={hkv} g={g} bs={bs}")
 
 
-def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device):
+@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
+def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device, hkv, g):
+    """q with padding heads (row stride past Hq * 128), one plan reused by
+    two calls, and a caller-owned output buffer; VALU (8 x 2) and MFMA
+    (2 x 8) kernels."""
     lens = [300, 1, 513, 256, 40]
-    dev, host, total = build_case(gpu_device, 8, 2, 256, lens, seed=7, q_pad_heads=16)
-    assert dev["q"].stride(0) == 32 * 128
+    dev, host, total = build_case(gpu_device, hkv, g, 256, lens, seed=7, q_pad_heads=16)
+    assert dev["q"].stride(0) == (hkv * g + 16) * 128
     plan = backend.build_attention_plan(dev["kc"], dev["cu"], total)
-    out = torch.empty((len(lens), 16, 128), dtype=torch.bfloat16, device=gpu_device)
+    out = torch.empty((len(lens), hkv * g, 128), dtype=torch.bfloat16, device=gpu_device)
     ref = reference(host, 0.1)
     for _ in range(2):
         out.zero_()
