@@ -648,9 +648,11 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
     int32_t row[kDecKeys / 4];
 #pragma unroll
     for (int i = 0; i < kDecKeys / 4; ++i) {
+      // Read unconditionally (the array holds whole chunks), so the four
+      // reads issue together; entries past nrows are never resolved.
       const int32_t t = key0 + 4 * i + g4;
-      const int32_t r = t < nrows ? sh.rows[t] : -1;
-      row[i] = r >= 0 ? r : 0;  // invalid: an in-bounds row, masked and zeroed later
+      const int32_t r = sh.rows[t];
+      row[i] = t < nrows && r >= 0 ? r : 0;  // invalid: an in-bounds row, masked and zeroed later
     }
 #pragma unroll
     for (int i = 0; i < kDecKeys / 4; ++i) {
@@ -724,7 +726,8 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
 #pragma unroll
       for (int i = 0; i < kDecKeys / 4; ++i) {
         const int32_t t = key0 + 4 * i + g4;
-        if (t >= nrows || sh.rows[t] < 0) v_tile[(4 * i + g4) * 16 + c16] = u32x4{0u, 0u, 0u, 0u};
+        const int32_t r = sh.rows[t];  // whole chunks: in the array
+        if (t >= nrows || r < 0) v_tile[(4 * i + g4) * 16 + c16] = u32x4{0u, 0u, 0u, 0u};
       }
     }
 
