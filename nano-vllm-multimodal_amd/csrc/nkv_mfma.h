@@ -84,6 +84,9 @@ __device__ __forceinline__ float row4_sum(float x) {
 // for it: a kernel waits for its copies itself (s_waitcnt on the vector
 // memory counter, which these copies count in, plus a barrier when other
 // wavefronts read the buffer) before it reads the buffer they fill.
+// M0 is a reserved register, so clang warns that a clobber of it may not be
+// preserved; in the kernels built from this file every M0 access is the
+// s_mov_b32 of these copies (no compiler value lives in M0 across them).
 // LDS byte address of a __shared__ array (a constant once inlined).
 __device__ __forceinline__ uint32_t lds_address(const u32x4* array) {
   typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
