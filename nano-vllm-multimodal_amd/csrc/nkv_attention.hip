@@ -24,8 +24,8 @@
 //   * q.k for the G query heads of that kv head is 4 v_dot2 on packed
 //     bf16 / fp16 pairs plus a 4-step DPP row sum (fp32);
 //   * an online softmax in fp32 with exp2 (scale * log2 e folded in);
-//   * the waves merge in LDS without a barrier: the last one to arrive
-//     stores the entry's partials (fp16 sums with a power-of-two scale).
+//   * the waves merge in LDS: after one barrier each wave merges and stores
+//     its share of the query heads (fp16 sums with a power-of-two scale).
 // At G <= 2 its VALU work stays under the memory time.
 //
 // MFMA kernel, G = 3..16 and any other kv-head count: one workgroup per
@@ -235,14 +235,13 @@ __device__ __forceinline__ void emit_partial(uint32_t* acc_out, f32x2* ml_out, f
 }
 
 // Shared state of one workgroup: the entry's cache rows, each wave's
-// partials, and the count of waves that have published theirs.
+// partials.
 template <int HQ>
 struct AttnShared {
   int32_t rows[kEntryRows];
   float acc[kAttnWaves][HQ][kHeadDim];
   float m[kAttnWaves][HQ];
   float l[kAttnWaves][HQ];
-  uint32_t arrived;
 };
 
 // Partials of plan entry blockIdx.x, for every query head qh:
@@ -255,10 +254,10 @@ struct AttnShared {
 // keeps the merge exact: both sums carry the same factor 2^(m + k - M).
 // An entry without valid rows gives (-inf, 0) and zeros.
 //
-// Epilogue without a barrier: each wave publishes its partials in LDS and
-// bumps an arrival counter; the last wave to arrive merges and stores them,
-// the others exit at once, so their slots go to the next workgroup instead
-// of idling until the slowest wave's loads return.
+// Epilogue: each wave publishes its partials in LDS; after one barrier the
+// waves split the query heads and merge and store them in parallel, which
+// ends the workgroup (and frees its LDS for the next) sooner than one wave
+// merging every head.
 template <int HKV, int G, bool kHalf>
 __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_seq_stride,
@@ -300,8 +299,7 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
     }
     sh.rows[t] = cache_row;
   }
-  if (threadIdx.x == 0) sh.arrived = 0u;
-  __syncthreads();  // rows resolved, counter zero, before any wave reads or arrives
+  __syncthreads();  // rows resolved before any wave reads them
 
   u32x4 qf[NC][G];
   const uint16_t* qs = q + static_cast<int64_t>(seq) * q_seq_stride;
@@ -462,21 +460,11 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
       }
     }
   }
-  // Publish (release), count the arrival; the wave that arrives last sees
-  // every other wave's partials after the acquire.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  uint32_t before = 0u;
-  if (lane == 0) {
-    before = __hip_atomic_fetch_add(&sh.arrived, 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  before = __builtin_amdgcn_readfirstlane(before);
-  if (before != kAttnWaves - 1) return;  // whole wavefront; no barrier follows
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-
-  // Per query head, two dims per lane: merge the waves against the largest
-  // reference, scale, store.
-  for (int qh = 0; qh < HQ; ++qh) {
+  // Every wave's partials are in LDS after the barrier; each wave then
+  // merges every kAttnWaves-th query head, two dims per lane, against the
+  // largest reference, scales and stores it.
+  __syncthreads();
+  for (int qh = wave; qh < HQ; qh += kAttnWaves) {
     float mm = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) mm = fmaxf(mm, sh.m[w][qh]);
@@ -513,8 +501,8 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
 // private ring of kDecSlots chunk buffers in LDS, filled by global_load_lds
 // kDecSlots - 1 chunks ahead of the one it computes and waited for with a
 // counted s_waitcnt (8 copies per chunk), so no barrier sits in the loop.
-// The waves then merge through LDS (the last to arrive stores the entry's
-// partials, as above), in the same format, for the same reduce kernel.
+// The waves then merge through LDS and split the stores of the query heads,
+// as above, in the same format, for the same reduce kernel.
 // Invalid rows (block id missing or outside the cache, keys past the entry)
 // copy cache row 0 into their slots; their scores are masked and their V
 // rows zeroed before the product.
@@ -557,7 +545,6 @@ union DecWaveMem {
 struct DecShared {
   DecWaveMem wave[kDecWaves];
   int32_t rows[(kEntryRows + kDecKeys - 1) / kDecKeys * kDecKeys];  // whole chunks
-  uint32_t arrived;
 };
 
 // s_waitcnt vmcnt(n) with the other counters left alone, and a compiler
@@ -608,7 +595,6 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
     }
     sh.rows[t] = cache_row;
   }
-  if (tid == 0) sh.arrived = 0u;
 
   // Q^T operands (B of S^T = K Q^T): lane holds head c16 of this kv head,
   // dims 32 dc + 8 g4 .. +8; zero for padding columns.
@@ -625,7 +611,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // q and the block ids have landed (nothing else in flight)
-  __syncthreads();                // rows resolved, counter zero
+  __syncthreads();                // rows resolved
 
   const uint32_t row_bytes = static_cast<uint32_t>(num_kv_heads) * kHeadBytes;
   const uint8_t* const k_head = key_cache + static_cast<int64_t>(kh) * kHeadBytes;
@@ -774,18 +760,9 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
       mine.part.l[c16] = acc[8][0];
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  uint32_t before = 0u;
-  if (lane == 0) {
-    before = __hip_atomic_fetch_add(&sh.arrived, 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  before = __builtin_amdgcn_readfirstlane(before);
-  if (before != kDecWaves - 1) return;  // whole wavefront; no barrier follows
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-
   const int64_t num_q_heads = static_cast<int64_t>(num_kv_heads) * group;
-  for (int g = 0; g < group; ++g) {
+  __syncthreads();  // every wave's partials are in LDS
+  for (int g = wave; g < group; g += kDecWaves) {
     float mm = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kDecWaves; ++w) mm = fmaxf(mm, sh.wave[w].part.m[g]);
