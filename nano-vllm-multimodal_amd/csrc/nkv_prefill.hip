@@ -334,14 +334,18 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
   // block ids loaded one tile before that (slots rotate over 4).
   int32_t ahead_block = -1;  // wavefront 0: block id of its lane's key in the next tile to resolve
   if (wave == 0) {
+    // The four block-id loads issue together, so the workgroup's start waits
+    // for one round trip through the table, not one per tile.
+    int32_t first_blocks[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) first_blocks[i] = i < num_tiles ? map.block_of(i * kPfKeys + lane) : -1;
+    if (num_tiles > 3) ahead_block = map.block_of(3 * kPfKeys + lane);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       if (i < num_tiles) {
-        resolve_rows(rows_buf[i], &invalid_buf[i], map, i * kPfKeys,
-                     map.block_of(i * kPfKeys + lane), lane);
+        resolve_rows(rows_buf[i], &invalid_buf[i], map, i * kPfKeys, first_blocks[i], lane);
       }
     }
-    if (num_tiles > 3) ahead_block = map.block_of(3 * kPfKeys + lane);
   }
   __syncthreads();
   issue_copies<kWide, false>(k_buf0, rows_buf[0], k_head, row_bytes, wave, lane);
