@@ -142,6 +142,16 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// Max over the 16 lanes of a DPP row, in every lane of the row (the same
+// four steps as row16_sum).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
@@ -220,9 +230,9 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(
 // carries the same factor, so the merge stays exact.
 __device__ __forceinline__ void emit_partial(uint32_t* acc_out, f32x2* ml_out, float a0, float a1,
                                              float mm, float lsum, int lane) {
-  float amax = fmaxf(fabsf(a0), fabsf(a1));
-#pragma unroll
-  for (int x = kWave / 2; x > 0; x >>= 1) amax = fmaxf(amax, __shfl_xor(amax, x, kWave));
+  // Largest magnitude of the head, in every lane: DPP within rows, then the
+  // cross-row swaps (VALU only, no LDS round trips).
+  const float amax = row4_max(row16_max(fmaxf(fabsf(a0), fabsf(a1))));
   const int e = static_cast<int>((__float_as_uint(amax) >> 23) & 0xFFu) - 127;
   const int k = amax > 0.f ? min(112, max(-112, e - 14)) : 0;
   const float down = __uint_as_float(static_cast<uint32_t>(127 - k) << 23);
