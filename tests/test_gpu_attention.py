@@ -241,6 +241,34 @@ def test_rows_outside_the_contexts_may_hold_any_bits(backend, gpu_device, hkv, g
     check_close(out, reference(host, scale), f"any-bits rows hkv={hkv} g={g}")
 
 
+@pytest.mark.parametrize("hkv,g", [(8, 2), (8, 4)])
+def test_cache_over_4gib(backend, gpu_device, hkv, g):
+    """Caches larger than 4 GiB, whose row byte offsets need more than 32
+    bits (the MFMA kernel's 64-bit-address instance; the VALU kernel always
+    forms 64-bit offsets): the contexts' blocks are moved to the top of each
+    cache."""
+    bs = 256
+    lens = [300, 700, 1, 513]
+    dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=43)
+    compact = dev["kc"].shape[0]
+    big = (1 << 32) // (bs * hkv * 128 * 2) + 8  # 4 GiB + 8 blocks per cache
+    shift = big - compact
+    kc = torch.empty((big, bs, hkv, 128), dtype=torch.bfloat16, device=gpu_device)
+    vc = torch.empty_like(kc)
+    try:
+        kc[:shift].zero_()
+        vc[:shift].zero_()
+        kc[shift:] = dev["kc"]
+        vc[shift:] = dev["vc"]
+        tables = torch.where(dev["tables"] >= 0, dev["tables"] + shift, dev["tables"])
+        scale = 1.0 / math.sqrt(128)
+        out = backend.paged_attention_decode(dev["q"], kc, vc, tables, dev["cu"], total, scale)
+        check_close(out, reference(host, scale), f"cache over 4 GiB hkv={hkv} g={g}")
+    finally:
+        del kc, vc
+        torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("hq", [16, 32])
 def test_decode_step_layer_full_size(backend, gpu_device, hq):
     """One layer of the 256-sequence decode step (contexts log-uniform in
