@@ -73,6 +73,9 @@ constexpr int kTileChunks = kPfKeys * 16;  // 16-byte chunks per K or V tile
 // plan order.  Plans of up to kPfSortMax tiles are sorted in LDS by one
 // workgroup (bitonic); longer ones list each sequence's tiles last tile
 // first, sequence after sequence.
+#ifndef NKV_PF_SETPRIO
+#define NKV_PF_SETPRIO 1  // raise the wave's priority over its MFMA block (0: never)
+#endif
 #ifndef NKV_PF_SORT_MAX
 #define NKV_PF_SORT_MAX 2048  // longest plan sorted in LDS (0: never sort)
 #endif
@@ -465,6 +468,11 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
         pb[c][mb] = w;
       }
     }
+#if NKV_PF_SETPRIO
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);  // this wave's MFMA phase goes first on the SIMD
+    __builtin_amdgcn_sched_barrier(0);
+#endif
     scores(k_next, st);
     // Scheduler order for the scores: four K operand reads ahead, then
     // each read's two MFMAs with the next read.
@@ -495,6 +503,11 @@ __global__ __launch_bounds__(kPfThreads, kPfBlocksPerCU) void attn_prefill_kerne
       acc[8][0] = E::mfma(ones, pb[c][0], acc[8][0]);
       acc[8][1] = E::mfma(ones, pb[c][1], acc[8][1]);
     }
+#if NKV_PF_SETPRIO
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+#endif
   };
   for (int32_t tile = 0; tile < num_tiles; tile += 2) {
     tile_step(std::integral_constant<int, 0>{}, tile);
