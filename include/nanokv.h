@@ -66,8 +66,9 @@ const char* nkv_last_error(void);
  *   store_cuda (csrc/paged_kv/paged_kv_cuda.cu:96-132); semantics of the
  *   pytorch oracle nanovllm/layers/paged_kv/pytorch_backend.py:26-38.
  * Strides are in elements (key.stride(0), value.stride(0)); row_elems is
- * kv_heads*head_dim (key.size(1)*key.size(2)); num_slots is
- * num_blocks*block_size of the cache.
+ * kv_heads*head_dim (key.size(1)*key.size(2)), and a token's row_elems
+ * elements must be contiguous (a view strided between heads is compacted by
+ * the caller first); num_slots is num_blocks*block_size of the cache.
  */
 int nkv_store(const void* key, const void* value, void* key_cache,
               void* value_cache, const int32_t* slot_mapping,
@@ -239,7 +240,8 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  * straight from the paged caches, with no gather.
  *   out[i, h, :] = softmax(scale * q[i, h] . K_i[:, h / G]^T) V_i[:, h / G]
  * for query head h, G = num_q_heads / num_kv_heads (kv head h / G), in fp32
- * with a result in the input type.  An empty context yields zeros.  dtype
+ * with a result in the input type; scale must be finite and positive
+ * (NKV_E_INVALID otherwise).  An empty context yields zeros.  dtype
  * NKV_DTYPE_BFLOAT16 or NKV_DTYPE_FLOAT16 (q, caches and out alike),
  * head_dim 128, any num_kv_heads, G <= 16.  G = 1 or 2 with 1, 2, 4 or 8
  * kv heads runs on the VALU kernel; every other layout runs on the MFMA

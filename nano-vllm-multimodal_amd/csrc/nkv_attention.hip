@@ -979,8 +979,13 @@ extern "C" int nkv_paged_attention_decode(
       out_seq_stride < num_q_heads * head_dim) {
     return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: bad sizes or strides");
   }
-  if (!std::isfinite(scale)) {
-    return nkv_fail(NKV_E_INVALID, "nkv_paged_attention_decode: scale must be finite");
+  // Both kernels rely on scale > 0: the MFMA kernel takes the chunk max of
+  // the raw scores (masked rows at -inf) before scaling, which commutes with
+  // a positive scale only (0 or a negative scale would turn masked rows into
+  // NaN or +inf weights).
+  if (!std::isfinite(scale) || !(scale > 0.f)) {
+    return nkv_fail(NKV_E_INVALID,
+                    "nkv_paged_attention_decode: scale must be finite and positive");
   }
   if (num_seqs == 0) return NKV_OK;
   const int64_t need = nkv_attention_workspace_bytes(capacity, num_q_heads, head_dim);

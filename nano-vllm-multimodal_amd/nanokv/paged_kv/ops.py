@@ -126,6 +126,14 @@ def _store_impl(key, value, key_cache, value_cache, slot_mapping) -> None:
     num_tokens = key.shape[0]
     if num_tokens == 0:
         return
+    # The kernel addresses a token's [kv_heads, head_dim] as one contiguous
+    # row through the token stride.  A head-strided view (e.g. kv[:, :, :128]
+    # of a [T, H, 256] tensor) passes the validators, which only require a
+    # contiguous last dimension, so it is compacted on the device first.
+    if key.shape[1] > 1 and key.stride(1) != key.shape[2]:
+        key = key.contiguous()
+    if value.shape[1] > 1 and value.stride(1) != value.shape[2]:
+        value = value.contiguous()
     library = _lib.load_library()
     status = library.nkv_store(
         key.data_ptr(),

@@ -67,6 +67,12 @@ def test_version_and_plan_geometry():
     (lambda l: l.nkv_build_gather_plan(None, 4, None, 9000, 10, 4, 8, 3, 1, None, 16, None), "num_seqs"),
     (lambda l: l.nkv_gather_varlen_planned(None, None, None, 4, 8, 8, 4, 8, 1, None, None, None), "null"),
     (lambda l: l.nkv_gather_varlen(None, None, None, 1, None, 2, 100, 16, 8, 4, 1, None, None, None, 16, None), "workspace"),
+    (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 8, 16, 128,
+                                            256, 16, 0.0, 1, None, 0, None, 2048, None), "positive"),
+    (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 2, 16, 128,
+                                            256, 16, -0.5, 1, None, 0, None, 2048, None), "positive"),
+    (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 8, 16, 128,
+                                            256, 16, float("nan"), 1, None, 0, None, 2048, None), "finite"),
     (lambda l: l.nkv_pack_decode(None, None, None, 0, 5000, 5000, 16, 4, 4, None, None, None, None, None), "num_seqs"),
     (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 3, 16, 4, 4, None, None, None, None, None), "null"),
     (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 2, 16, 4, 4, None, None, None, None, None), "padded_seqs"),

@@ -107,6 +107,24 @@ def test_registered_ops_dispatch_to_hip(backend, gpu_device):
     np.testing.assert_array_equal(words(v_out), expect_v)
 
 
+def test_store_of_head_strided_views(backend, gpu_device):
+    """A view strided between heads (kv[:, :, :128] of a [T, H, 256]
+    tensor) passes the validators, which only ask for a contiguous last
+    dimension; the store must still copy each head's own 128 elements, as
+    the pytorch backend's index_copy_ does."""
+    torch.manual_seed(43)
+    wide = torch.randn(11, 4, 256, device=gpu_device, dtype=torch.bfloat16)
+    key, value = wide[:, :, :128], wide[:, :, 128:]
+    assert key.stride(1) == 256 and key.stride(-1) == 1
+    slots = torch.tensor([3, -1, 40, 7, 63, 0, 22, 9, 51, -1, 30], dtype=torch.int32, device=gpu_device)
+    kc = torch.full((4, 16, 4, 128), -3, device=gpu_device, dtype=torch.bfloat16)
+    vc = torch.full_like(kc, -3)
+    hk, hv = oracle_store(key.contiguous(), value.contiguous(), kc, vc, slots)
+    backend.store(key, value, kc, vc, slots)
+    np.testing.assert_array_equal(words(kc), hk)
+    np.testing.assert_array_equal(words(vc), hv)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_legacy_store_kvcache_on_fused_qkv(gpu_device, dtype):
     """attention.py:10-33 / :86-93: the layer's fallback store when no
