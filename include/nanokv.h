@@ -171,6 +171,30 @@ int nkv_gather_varlen(const void* key_cache, const void* value_cache,
                       int64_t workspace_bytes, void* stream);
 
 /*
+ * nkv_gather_varlen without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops and harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Same arguments
+ * and result as nkv_gather_varlen minus the workspace: the plan lives in a
+ * device array inside the library (NKV_SCRATCH_BYTES per GPU, held until
+ * the process ends), so the call allocates nothing.  A plan larger than the
+ * array (nkv_gather_plan_capacity(...) * 16 > NKV_SCRATCH_BYTES, i.e. about
+ * 4.2 million rows of 2 KiB) is rejected with NKV_E_CAPACITY before any
+ * device work.  The device is the calling thread's current device, which
+ * must own `stream`.  Every call on one GPU uses that GPU's one array:
+ * calls that overlap on the same GPU (different streams without ordering,
+ * or concurrent threads) race and must not be issued; calls on one stream
+ * are ordered and safe.
+ */
+#define NKV_SCRATCH_BYTES (4 << 20)
+int nkv_gather_varlen_noalloc(const void* key_cache, const void* value_cache,
+                              const int32_t* block_tables, int64_t table_stride,
+                              const int32_t* cu_seqlens_k, int64_t num_seqs,
+                              int64_t total_rows, int64_t block_size,
+                              int64_t row_elems, int64_t num_blocks,
+                              int32_t dtype, void* key_out, void* value_out,
+                              void* stream);
+
+/*
  * Decode-step metadata packing on the device.  Input is the scheduler's
  * per-sequence state in CSR form: num_tokens[i] (len(seq)), and the block
  * list of sequence i = block_ids[block_offsets[i] .. block_offsets[i+1]);

@@ -64,6 +64,13 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
             c_i32, c_ptr, c_ptr, c_ptr, c_i64, c_ptr,
         ),
     ),
+    "nkv_gather_varlen_noalloc": (
+        ctypes.c_int,
+        (
+            c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64,
+            c_i32, c_ptr, c_ptr, c_ptr,
+        ),
+    ),
     "nkv_pack_decode": (
         ctypes.c_int,
         (c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr),
@@ -140,6 +147,7 @@ NKV_DTYPE_BFLOAT16 = 1
 NKV_DTYPE_FLOAT32 = 2
 NKV_MAX_PLAN_SEQS = 8192
 NKV_MAX_PACK_SEQS = 4096
+NKV_SCRATCH_BYTES = 4 << 20
 
 _LOCK = Lock()
 _LIBRARY: ctypes.CDLL | None = None

@@ -27,6 +27,7 @@ SOURCES = (
     "nkv_attention.hip",
     "nkv_prefill.hip",
     "nkv_pool.hip",
+    "nkv_noalloc.hip",
 )
 OFFLOAD_ARCH = "gfx950"
 HIPCC_FLAGS = (

@@ -67,6 +67,8 @@ def test_version_and_plan_geometry():
     (lambda l: l.nkv_build_gather_plan(None, 4, None, 9000, 10, 4, 8, 3, 1, None, 16, None), "num_seqs"),
     (lambda l: l.nkv_gather_varlen_planned(None, None, None, 4, 8, 8, 4, 8, 1, None, None, None), "null"),
     (lambda l: l.nkv_gather_varlen(None, None, None, 1, None, 2, 100, 16, 8, 4, 1, None, None, None, 16, None), "workspace"),
+    (lambda l: l.nkv_gather_varlen_noalloc(None, None, None, 1, None, 2, 10**8, 256, 1024, 4, 1, None, None, None), "scratch"),
+    (lambda l: l.nkv_gather_varlen_noalloc(None, None, None, 1, None, 2, -1, 256, 1024, 4, 1, None, None, None), "non-negative"),
     (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 8, 16, 128,
                                             256, 16, 0.0, 1, None, 0, None, 2048, None), "positive"),
     (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 2, 16, 128,
