@@ -6,13 +6,20 @@
 // (row = one (block, in-block slot) pair of the [num_blocks, block_size,
 // kv_heads, head_dim] cache).  K and V are moved by the same launch.
 //
-// Launch shape: the one measured best for paged-KV copies on MI355X (see
-// nkv_gather.hip): short-lived 128-thread workgroups, each moving ~4 KiB of
-// ONE tensor (K rows in blockIdx.y == 0, V rows in blockIdx.y == 1) with
-// one 16-byte word in flight per lane and non-temporal accesses.  A
+// Launch shape (measured on MI355X with rocprofv3 on the chunked-prefill
+// store, 67 MB, and the narrow-row store, 107 MB): short-lived 128-thread
+// workgroups, each moving ~4 KiB of ONE tensor (K rows in blockIdx.y == 0,
+// V rows in blockIdx.y == 1) in one batch, with non-temporal accesses.  A
 // workgroup takes rows_per_wg consecutive tokens (2 rows of 2 KiB, 8 of
-// 512 B); consecutive lanes move consecutive words of a row.  The work is
-// pure bandwidth (no MFMA, no LDS).
+// 512 B); consecutive lanes move consecutive words of a row.  Each lane
+// issues its data loads together with its slot loads, one memory round
+// trip per batch instead of two (-2 to -4%).  Workgroup size (64-512
+// threads), bytes per workgroup (2-16 KiB), an XCD-contiguous workgroup
+// order and ordinary (cached) stores change the steady-state rate of
+// back-to-back stores by under 3%; ordinary stores look up to 10% faster
+// when each launch is timed alone after a cache eviction, because the
+// 256 MB MALL then absorbs the launch's writes and their write-back falls
+// outside it.  The work is pure bandwidth (no MFMA, no LDS).
 #include "nkv_common.h"
 
 namespace nkv {
@@ -25,11 +32,40 @@ namespace {
 #define NKV_STORE_WG_BYTES 4096
 #endif
 
+// 1: a lane issues its rows' data loads together with their slot loads (one
+// memory round trip per batch; a row whose slot turns out invalid has been
+// read for nothing, which only -1 padding rows cost).  0: data loads wait
+// for the slots and skip invalid rows.
+#ifndef NKV_STORE_SPECULATIVE
+#define NKV_STORE_SPECULATIVE 1
+#endif
+
+// Cache policy of the K/V reads and of the cache writes (1 = non-temporal).
+#ifndef NKV_STORE_NT_LOADS
+#define NKV_STORE_NT_LOADS 1
+#endif
+#ifndef NKV_STORE_NT_STORES
+#define NKV_STORE_NT_STORES 1
+#endif
+
+template <typename T>
+__device__ __forceinline__ T store_src_load(const T* p) {
+  if constexpr (NKV_STORE_NT_LOADS) return load_stream(p);
+  return *p;
+}
+template <typename T>
+__device__ __forceinline__ void store_dst_store(T* p, T v) {
+  if constexpr (NKV_STORE_NT_STORES) {
+    store_stream(p, v);
+  } else {
+    *p = v;
+  }
+}
+
 constexpr int kStoreThreads = NKV_STORE_THREADS;
 
 // Words per lane issued together: one workgroup's NKV_STORE_WG_BYTES in one
-// batch, so a lane waits for memory twice per batch (its rows' slots, then
-// its words) instead of twice per word.
+// batch, so a lane waits for memory once per batch instead of once per word.
 template <int W>
 constexpr int store_batch() {
   return NKV_STORE_WG_BYTES / (W * kStoreThreads) > 0
@@ -63,15 +99,18 @@ __global__ __launch_bounds__(kStoreThreads) void store_rows_kernel(
     T v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      // -1 padding (and any slot outside the cache) moves nothing
-      if (slot[u] >= 0 && slot[u] < num_slots) {
-        v[u] = load_stream(reinterpret_cast<const T*>(src + (t0 + row[u]) * stride) + col[u]);
+      const int32_t w = base + u * kStoreThreads + static_cast<int32_t>(threadIdx.x);
+      // -1 padding (and any slot outside the cache) is never stored; with
+      // NKV_STORE_SPECULATIVE its row is still read (in bounds: t < num_tokens)
+      const bool load = NKV_STORE_SPECULATIVE ? w < nwords : (slot[u] >= 0 && slot[u] < num_slots);
+      if (load) {
+        v[u] = store_src_load(reinterpret_cast<const T*>(src + (t0 + row[u]) * stride) + col[u]);
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (slot[u] >= 0 && slot[u] < num_slots) {
-        store_stream(reinterpret_cast<T*>(dst + slot[u] * row_bytes) + col[u], v[u]);
+        store_dst_store(reinterpret_cast<T*>(dst + slot[u] * row_bytes) + col[u], v[u]);
       }
     }
   }
