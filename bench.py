@@ -37,7 +37,6 @@ from __future__ import annotations
 import argparse
 import json
 import math
-import platform
 import sys
 import time
 from pathlib import Path
@@ -48,23 +47,49 @@ for _p in (REPO_ROOT, REPO_ROOT / "nano-vllm-multimodal_amd"):
         sys.path.insert(0, str(_p))
 
 METRIC = "paged KV store+gather GB/s (fraction of HBM peak); decode-step tokens/s, 1 GPU"
-TRAFFIC_FILE = REPO_ROOT / "profiles" / "gather_varlen_decode_step_traffic.json"
-ATTENTION_TRAFFIC_FILE = REPO_ROOT / "profiles" / "paged_attention_decode_step_traffic.json"
+# Cases of the profiling replay (--case): the four single-layer
+# configurations, the full decode step (store + gather) and the decode step
+# with paged-attention decode in place of the gather.
+PROFILE_CASES = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows", "decode_step",
+                 "decode_attention")
 
 
-def measured_traffic(path: Path, algorithmic_bytes: int):
-    """HBM bytes per launch from a committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (calibrated against a copy of known size), or None
-    unless it was measured on this workload (same algorithmic bytes)."""
+PROFILE_FILE = REPO_ROOT / "profiles" / "decode_step_rocprof.json"
+ATTENTION_PROFILE_FILE = REPO_ROOT / "profiles" / "decode_attention_rocprof.json"
+
+
+def profiled_median(path: Path, kernel_prefix: str, algorithmic_bytes: int):
+    """Median per-dispatch duration (µs) of a kernel in a committed
+    rocprofv3 summary (written by ``python -m nanokv.profiling report``),
+    or None unless it was profiled on this workload (same algorithmic
+    bytes per launch)."""
     if not path.is_file():
         return None
     try:
-        t = json.loads(path.read_text())
+        kernels = json.loads(path.read_text()).get("kernels", {})
     except (OSError, ValueError):
         return None
-    if (t.get("workload") == "decode_step" and t.get("layers_per_launch") == 1
-            and t.get("algorithmic_bytes_per_launch") == algorithmic_bytes):
-        return t.get("bytes_per_launch")
+    for name, record in kernels.items():
+        if name.startswith(kernel_prefix) and record.get("algorithmic_bytes") == algorithmic_bytes:
+            return round(record["median_us"], 2)
+    return None
+
+
+def measured_traffic(path: Path, kernel_prefix: str, algorithmic_bytes: int):
+    """HBM bytes per launch of a kernel (FETCH_SIZE + WRITE_SIZE, each scaled
+    by its reading for a copy of known size) from a committed rocprofv3
+    summary, or None unless the summary was taken on this workload (same
+    algorithmic bytes per launch)."""
+    if not path.is_file():
+        return None
+    try:
+        kernels = json.loads(path.read_text()).get("kernels", {})
+    except (OSError, ValueError):
+        return None
+    for name, record in kernels.items():
+        if (name.startswith(kernel_prefix) and record.get("algorithmic_bytes") == algorithmic_bytes
+                and "traffic_bytes" in record):
+            return record["traffic_bytes"]
     return None
 
 
@@ -76,8 +101,10 @@ def parse_args(argv=None):
     p.add_argument("--layers", type=int, default=28)
     p.add_argument("--check-layers", default="0", help="comma list of layers checked vs the oracle; '' = none")
     p.add_argument("--cpu-baseline-layers", type=int, default=28,
-                   help="layers in the CPU baseline sample (0 disables it)")
-    p.add_argument("--cpu-baseline-repeats", type=int, default=9)
+                   help="decode-step layers in the CPU baseline sample of the reference's torch "
+                        "ops (0 disables the CPU leg)")
+    p.add_argument("--cpu-baseline-repeats", type=int, default=3,
+                   help="runs of the 28-layer step in the OpenMP port's figure")
     p.add_argument("--workload-iterations", type=int, default=30,
                    help="timed launches per operation of the single-layer configurations; 0 = skip")
     p.add_argument("--no-gpu-reference", dest="gpu_reference", action="store_false",
@@ -90,7 +117,28 @@ def parse_args(argv=None):
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="only run a plain device copy of this many MiB 3 times (the known-size "
                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
-    return p.parse_args(argv)
+    p.add_argument("--case", choices=PROFILE_CASES,
+                   help="with --profile-replay: the one case to replay for a profiler")
+    p.add_argument("--profile-replay", type=int, default=0, metavar="N",
+                   help="check --case once against the reference backend, replay it N times "
+                        "with no events (a MALL eviction before every launch of the single-layer "
+                        "cases), print one line, exit")
+    p.add_argument("--cpu-baseline-workloads", default="decode_store,chunked_prefill,prefix_gather,narrow_rows",
+                   help="single-layer configurations the CPU baseline also times ('' = none)")
+    args = p.parse_args(argv)
+    if bool(args.case) != bool(args.profile_replay):
+        p.error("--case and --profile-replay go together")
+    if args.profile_replay < 0:
+        p.error("--profile-replay must be positive")
+    return args
+
+
+def reference_backend():
+    """The torch restatement of the reference pytorch backend
+    (nanokv.benchmark.TorchReferenceBackend)."""
+    from nanokv.benchmark import TorchReferenceBackend
+
+    return TorchReferenceBackend()
 
 
 def log(msg: str) -> None:
@@ -110,7 +158,8 @@ def main(argv=None) -> int:
     import torch
 
     from nanokv import workloads
-    from nanokv.benchmark import MI355X_HBM_PEAK_GBPS, LaunchTimer, effective_bytes, summarize_latencies
+    from nanokv.benchmark import (MI355X_HBM_PEAK_GBPS, LaunchTimer, effective_bytes, environment_identity,
+                                  summarize_latencies)
     from nanokv.packing import DevicePacker, SequenceBatch
     from nanokv.paged_kv import create_paged_kv_backend
 
@@ -127,6 +176,12 @@ def main(argv=None) -> int:
         print(json.dumps({"copy_calibration_bytes": n, "launches": 3}), flush=True)
         return 0
     backend = create_paged_kv_backend("hip")
+    if args.case in ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows"):
+        from nanokv.benchmark import replay_workload
+
+        replay_workload(args.case, args.profile_replay, device)
+        print(f"profile replay complete: {args.case} x {args.profile_replay}", flush=True)
+        return 0
     if args.prefill_only:
         print(json.dumps(measure_prefill_attention(device, backend, args.steps)), flush=True)
         return 0
@@ -188,6 +243,70 @@ def main(argv=None) -> int:
                 timer.stop(t0)
         return ctx
 
+    host_cu = wl.cu_seqlens_k().tolist()
+
+    def check_layer(layer: int) -> None:
+        """Layer ``layer`` of the step (store, then varlen gather) against
+        the torch restatement of the reference backend on copies of the
+        layer's caches, bit-exact."""
+        ref = reference_backend()
+        ctx = packer.pack_decode(batch)
+        kc, vc = cache[0, layer], cache[1, layer]
+        expect_k, expect_v = kc.clone(), vc.clone()
+        ref.store(new_k[layer], new_v[layer], expect_k, expect_v, ctx.slot_mapping)
+        plan = backend.build_gather_plan(kc, ctx.block_tables, ctx.cu_seqlens_k, total)
+        backend.store(new_k[layer], new_v[layer], kc, vc, ctx.slot_mapping)
+        backend.gather_varlen(kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total, plan=plan,
+                              out=(k_out, v_out))
+        words = torch.int16
+        if not (torch.equal(kc.view(words), expect_k.view(words))
+                and torch.equal(vc.view(words), expect_v.view(words))):
+            raise AssertionError(f"decode step layer {layer}: store differs from the reference backend")
+        for i, n in enumerate(wl.num_tokens.tolist()):
+            for expect, out in ((expect_k, k_out), (expect_v, v_out)):
+                got = out[host_cu[i]:host_cu[i] + n].view(words)
+                if not torch.equal(got, ref.gather(expect, ctx.block_tables[i], n).view(words)):
+                    raise AssertionError(f"decode step layer {layer}: gather of sequence {i} differs")
+        del expect_k, expect_v
+
+    def check_attention(layer: int, sample: int = 8) -> None:
+        """Paged-attention decode of ``sample`` sequences of layer
+        ``layer`` against a float32 softmax(q K^T) V on the host over the
+        same K/V rows (gathered bit-exactly above)."""
+        ctx = packer.pack_decode(batch)
+        kc, vc = cache[0, layer], cache[1, layer]
+        backend.gather_varlen(kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total, out=(k_out, v_out))
+        backend.paged_attention_decode(q, kc, vc, ctx.block_tables, ctx.cu_seqlens_k, total,
+                                       softmax_scale, out=attn_out)
+        torch.cuda.synchronize(device)
+        group = num_q_heads // wl.num_kv_heads
+        for i in np.linspace(0, B - 1, sample).astype(int).tolist():
+            lo, n = host_cu[i], int(wl.num_tokens[i])
+            # [heads, rows, dim] per query head (kv head h // group), float32 on the host
+            keys = k_out[lo:lo + n].float().cpu().repeat_interleave(group, dim=1).transpose(0, 1)
+            values = v_out[lo:lo + n].float().cpu().repeat_interleave(group, dim=1).transpose(0, 1)
+            query = q[i].float().cpu().unsqueeze(-1)
+            weights = torch.softmax(torch.matmul(keys, query).squeeze(-1) * softmax_scale, dim=-1)
+            expect = torch.matmul(weights.unsqueeze(1), values).squeeze(1)
+            err = (attn_out[i].float().cpu() - expect).abs()
+            if bool((err > 1e-3 + 1e-2 * expect.abs()).any()):
+                raise AssertionError(f"decode attention, sequence {i}: max error {float(err.max()):.3e}")
+
+    if args.case == "decode_step":
+        check_layer(0)
+        for _ in range(args.profile_replay):
+            step()
+        torch.cuda.synchronize(device)
+        print(f"profile replay complete: decode_step x {args.profile_replay}", flush=True)
+        return 0
+    if args.case == "decode_attention":
+        check_attention(0)
+        for _ in range(args.profile_replay):
+            attention_step()
+        torch.cuda.synchronize(device)
+        print(f"profile replay complete: decode_attention x {args.profile_replay}", flush=True)
+        return 0
+
     # -------------------------------------------------------------- timed steps
     for _ in range(args.warmup):
         step()
@@ -203,6 +322,24 @@ def main(argv=None) -> int:
     wall_s = time.perf_counter() - t0
     step_ms = start_evt.elapsed_time(end_evt) / args.steps
     log(f"[bench] {args.steps} steps: {step_ms:.3f} ms/step (wall {wall_s * 1000 / args.steps:.3f})")
+    # The dominant kernel on its own, at the rate it runs inside the step:
+    # the same varlen gathers back to back over the 28 layers' caches, one
+    # event pair around them (the host enqueues a call far faster than the
+    # ~1 ms kernel runs, so the stream never idles and no per-launch
+    # instrumentation is counted).
+    ctx = packer.pack_decode(batch)
+    plan = backend.build_gather_plan(cache[0, 0], ctx.block_tables, ctx.cu_seqlens_k, total)
+    torch.cuda.synchronize()
+    start_evt.record(stream)
+    for _ in range(args.steps):
+        for layer in range(L):
+            backend.gather_varlen(cache[0, layer], cache[1, layer], ctx.block_tables, ctx.cu_seqlens_k,
+                                  total, plan=plan, out=(k_out, v_out))
+    end_evt.record(stream)
+    torch.cuda.synchronize()
+    gather_launch_us = start_evt.elapsed_time(end_evt) * 1e3 / (args.steps * L)
+    log(f"[bench] gather back to back: {gather_launch_us:.1f} us per launch "
+        f"(x {L} = {gather_launch_us * L / 1e3:.3f} ms of the {step_ms:.3f} ms step)")
     # Per-kernel breakdown in a pass of its own: the event pairs around each
     # launch are instrumentation, so they stay out of the timed steps above.
     timer = LaunchTimer(stream)
@@ -225,7 +362,38 @@ def main(argv=None) -> int:
     for _ in range(args.steps):
         attention_step(attn_timer)
     attn_us = attn_timer.durations_us()
-    attn_mean = sum(attn_us) / len(attn_us)
+    # per call at the rate it runs inside the step: back to back over the
+    # 28 layers' caches, one event pair around them
+    actx = packer.pack_decode(batch)
+    aplan = backend.build_attention_plan(cache[0, 0], actx.cu_seqlens_k, total)
+    torch.cuda.synchronize()
+    start_evt.record(stream)
+    for _ in range(args.steps):
+        for layer in range(L):
+            backend.paged_attention_decode(q, cache[0, layer], cache[1, layer], actx.block_tables,
+                                           actx.cu_seqlens_k, total, softmax_scale, plan=aplan,
+                                           out=attn_out)
+    end_evt.record(stream)
+    torch.cuda.synchronize()
+    attn_mean = start_evt.elapsed_time(end_evt) * 1e3 / (args.steps * L)
+    # The flash_attn_with_kvcache drop-in on the same contexts: it takes only
+    # the lengths tensor, so it sizes its plan for the tables' full width
+    # (no host read of the lengths).
+    from nanokv.flash import flash_attn_with_kvcache
+
+    q4 = q.unsqueeze(1)
+    flash_attn_with_kvcache(q4, cache[0, 0], cache[1, 0], cache_seqlens=actx.context_lens,
+                            block_table=actx.block_tables, softmax_scale=softmax_scale, causal=True)
+    torch.cuda.synchronize()
+    start_evt.record(stream)
+    for _ in range(args.steps):
+        for layer in range(L):
+            flash_attn_with_kvcache(q4, cache[0, layer], cache[1, layer], cache_seqlens=actx.context_lens,
+                                    block_table=actx.block_tables, softmax_scale=softmax_scale,
+                                    causal=True)
+    end_evt.record(stream)
+    torch.cuda.synchronize()
+    flash_us = start_evt.elapsed_time(end_evt) * 1e3 / (args.steps * L)
     attn_bytes = (total * wl.num_kv_heads * wl.head_dim * 2 * q.element_size()
                   + 2 * q.numel() * q.element_size())
     log(f"[bench] {args.steps} store+attention steps: {attn_step_ms:.3f} ms/step, "
@@ -238,8 +406,12 @@ def main(argv=None) -> int:
     gather_launch_bytes = wl.gather_bytes(layers=1)
     gather_us = timer.durations_us()
     store_us = store_timer.durations_us()
-    gather_mean = sum(gather_us) / len(gather_us)
-    achieved = gather_launch_bytes / (gather_mean * 1e-6) / 1e9
+    achieved = gather_launch_bytes / (gather_launch_us * 1e-6) / 1e9
+    consistent = L * gather_launch_us <= step_ms * 1e3
+    if not consistent:
+        log(f"[bench] WARNING: {L} x {gather_launch_us:.1f} us of back-to-back gathers exceed the "
+            f"{step_ms:.3f} ms step")
+    profiled = profiled_median(PROFILE_FILE, "gather_planned_kernel", gather_launch_bytes)
 
     copy_reference = measure_copy_reference(wl, device, backend, packer, cache, total, k_out, v_out,
                                             args.steps)
@@ -284,8 +456,8 @@ def main(argv=None) -> int:
                 log(f"[bench] {r['workload']} {r['operation']}: p50 {r['p50_us']:.2f} us, "
                     f"{r['gbps_at_p50']:.0f} GB/s")
 
-    traffic = measured_traffic(TRAFFIC_FILE, wl.gather_bytes(layers=1))
-    attn_traffic = measured_traffic(ATTENTION_TRAFFIC_FILE, attn_bytes)
+    traffic = measured_traffic(PROFILE_FILE, "gather_planned_kernel", wl.gather_bytes(layers=1))
+    attn_traffic = measured_traffic(ATTENTION_PROFILE_FILE, "attn_decode_partial_kernel", attn_bytes)
 
     cpu_baseline = None
     if not args.profile and args.cpu_baseline_layers > 0:
@@ -316,7 +488,8 @@ def main(argv=None) -> int:
                     "q": q.float().cpu().numpy(), "scale": softmax_scale}
 
         cpu_baseline = cpu_baseline_leg(wl, args.cpu_baseline_layers, args.cpu_baseline_repeats,
-                                        check_layers, gpu_layer)
+                                        check_layers, gpu_layer,
+                                        args.cpu_baseline_workloads.split(","))
 
     result = {
         "metric": METRIC,
@@ -351,6 +524,8 @@ def main(argv=None) -> int:
             effective_bytes("store", B, wl.num_kv_heads, wl.head_dim, 2)
             + 2 * effective_bytes("gather", total, wl.num_kv_heads, wl.head_dim, 2)),
         "kernels": {
+            "note": "per-launch event pairs in a pass of their own (each includes the time from "
+                    "the start event to the kernel's start); the roofline uses the back-to-back rate",
             "gather_varlen_planned_us": summarize_latencies(gather_us),
             "store_us": summarize_latencies(store_us),
         },
@@ -362,21 +537,32 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / MI355X_HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "traffic_source": "profiles/gather_varlen_decode_step_traffic.json" if traffic else None,
+            "traffic_source": (str(PROFILE_FILE.relative_to(REPO_ROOT)) if traffic else None),
             "algorithmic_bytes_per_launch": gather_launch_bytes,
+            "us_per_launch": round(gather_launch_us, 2),
+            "timing": f"{args.steps} x {L} gathers back to back over the layers' caches, one event "
+                      f"pair around them, on the stream the kernel runs on",
+            "launches_per_step_us": round(L * gather_launch_us, 1),
+            "within_step": consistent,
+            "rocprof_median_us": profiled,
+            "rocprof_source": str(PROFILE_FILE.relative_to(REPO_ROOT)) if profiled else None,
         },
         "attention": {
             "kernel": "paged_attention_decode (split-K partials + merge, one layer, 16 q heads "
                       "over 8 kv heads, straight from the paged cache)",
-            "us": summarize_latencies(attn_us),
+            "us_bracketed": summarize_latencies(attn_us),
             "achieved": round(attn_bytes / (attn_mean * 1e-6) / 1e9, 2),
             "peak": MI355X_HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(attn_bytes / (attn_mean * 1e-6) / 1e9 / MI355X_HBM_PEAK_GBPS, 4),
             "algorithmic_bytes_per_launch": attn_bytes,
             "traffic": attn_traffic,
-            "traffic_source": ("profiles/paged_attention_decode_step_traffic.json"
+            "traffic_source": (str(ATTENTION_PROFILE_FILE.relative_to(REPO_ROOT))
                                if attn_traffic else None),
+            "us_per_call": round(attn_mean, 2),
+            "timing": "calls back to back over the layers' caches (plan built once), one event pair",
+            "flash_attn_with_kvcache_us_per_call": round(flash_us, 2),
+            "flash_dropin_over_direct": round(flash_us / attn_mean, 4),
             "step_ms_store_attention": round(attn_step_ms, 4),
             "decode_tokens_per_s_store_attention": round(B / (attn_step_ms * 1e-3), 2),
         },
@@ -387,8 +573,8 @@ def main(argv=None) -> int:
         "gpu_reference": gpu_reference,
         "block_pool": block_pool,
         "cpu_baseline": cpu_baseline,
-        "host": {"platform": platform.platform(), "torch": torch.__version__, "hip": torch.version.hip,
-                 "gpu": torch.cuda.get_device_name(device)},
+        "report_schema": "nanokv.paged_kv_bench.v2",
+        "identity": environment_identity(device),
     }
     print(json.dumps(result), flush=True)
     return 0
@@ -532,7 +718,7 @@ def measure_prefill_attention(device, backend, reps: int) -> dict:
     us = timer.durations_us()[0] / reps
     pairs = sum(sum(lk - lq + j + 1 for j in range(lq)) for lq, lk in zip(q_lens, k_lens))
     flops = 4 * dim * hkv * g * pairs
-    ref = torch_reference_backend()
+    ref = reference_backend()
 
     def sdpa_path():
         for i, (lq, lk) in enumerate(zip(q_lens, k_lens)):
@@ -574,9 +760,13 @@ OTHER_WORKLOADS = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_r
 def measure_other_workloads(device, iterations: int) -> list[dict]:
     """The single-layer store / gather configurations of the paged-KV
     micro-benchmark (decode store, chunked-prefill store, prefix-cache
-    gather, narrow rows), each on its own cache, with the MALL evicted by a
-    512 MiB read before every timed launch.  One compact record per
-    operation that moves bytes."""
+    gather, narrow rows), each on its own cache, checked bit-exactly against
+    the reference backend's torch ops first.  Two timings per operation:
+    p50 of per-launch event pairs with the MALL evicted by a 512 MiB read
+    before every launch (the reference benchmark's per-iteration method),
+    and the steady-state rate of launches back to back over 16 rotating
+    disjoint input/output sets (write-backs of earlier launches included).
+    One compact record per operation that moves bytes."""
     import torch
 
     from nanokv.benchmark import run_workload
@@ -591,6 +781,7 @@ def measure_other_workloads(device, iterations: int) -> list[dict]:
                 "algorithmic_bytes": r["algorithmic_bytes"],
                 "p50_us": round(r["latency"]["p50_us"], 2),
                 "gbps_at_p50": r["gbps_at_p50"], "hbm_fraction": r["hbm_fraction"],
+                "steady_state": r.get("steady_state"),
             })
         torch.cuda.empty_cache()
     return records
@@ -765,37 +956,6 @@ def measure_block_pool(wl, device, packer, batch, steps: int, warmup: int) -> di
     }
 
 
-def torch_reference_backend():
-    """The reference's ``pytorch`` paged-KV backend
-    (nanovllm/layers/paged_kv/pytorch_backend.py:26-50) restated with the
-    same validators and the same torch ops, for timing on the GPU beside the
-    hip backend: the store masks out -1 slots (a device-to-host sync) and
-    scatters with ``index_copy_``; the gather copies whole blocks with
-    ``index_select`` and slices them to the length."""
-    import torch
-
-    from nanokv.paged_kv import validate_gather_inputs, validate_store_inputs
-
-    class TorchReferenceBackend:
-        name = "torch-reference"
-
-        def store(self, key, value, key_cache, value_cache, slot_mapping):
-            validate_store_inputs(key, value, key_cache, value_cache, slot_mapping)
-            keep = slot_mapping >= 0
-            rows = slot_mapping[keep].to(dtype=torch.long)
-            key_cache.flatten(0, 1).index_copy_(0, rows, key[keep])
-            value_cache.flatten(0, 1).index_copy_(0, rows, value[keep])
-
-        def gather(self, cache, block_table, sequence_length):
-            dims = validate_gather_inputs(cache, block_table, sequence_length)
-            if dims.required_blocks == 0:
-                return cache.new_empty((0, dims.num_kv_heads, dims.head_dim))
-            ids = block_table[: dims.required_blocks].to(dtype=torch.long)
-            return cache.index_select(0, ids).flatten(0, 1)[:sequence_length]
-
-    return TorchReferenceBackend()
-
-
 def measure_torch_reference_step(wl, device, cache, new_k, new_v, batch, packer,
                                  hip_step_ms: float, steps: int = 2) -> dict:
     """The decode step's data path as the reference's SDPA decode drives its
@@ -806,7 +966,7 @@ def measure_torch_reference_step(wl, device, cache, new_k, new_v, batch, packer,
     the host).  The outputs are dropped where SDPA would consume them."""
     import torch
 
-    ref = torch_reference_backend()
+    ref = reference_backend()
     ctx = packer.pack_decode(batch)
     torch.cuda.synchronize()
 
@@ -859,7 +1019,7 @@ def measure_reference_matrix(device, backend, iterations: int | None = None) -> 
 
     m = REFERENCE_MATRIX
     iterations = iterations or m["iterations"]
-    ref = torch_reference_backend()
+    ref = reference_backend()
     dtypes = {"float16": torch.float16, "bfloat16": torch.bfloat16}
     words = {torch.float16: torch.int16, torch.bfloat16: torch.int16}
     records = []
@@ -922,11 +1082,14 @@ def measure_reference_matrix(device, backend, iterations: int | None = None) -> 
             "iterations": iterations, "warmup": m["warmup"]}
 
 
-def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer) -> dict:
+def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer,
+                     workload_names) -> dict:
     """The CPU leg: the oracle checks the GPU's outputs of ``check_layers``
     (store+gather bit-exact; attention within 1e-3 + 1e-2*|ref| of the fp32
-    oracle on 32 sequences), then its C restatement is timed on the host
-    cores (:func:`run_cpu_baseline`)."""
+    oracle on 32 sequences); then the reference pytorch backend's torch ops
+    are timed on host tensors (:func:`cpu_reference_baseline`, the figure
+    the line reports), and the oracle's OpenMP C restatement beside them
+    (:func:`openmp_port_baseline`)."""
     import numpy as np
     import torch
 
@@ -961,8 +1124,9 @@ def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer) -> 
                                  f"(max err {err.max():.3e})")
         log(f"[bench] layer {layer}: store+gather bit-exact, attention max err {err.max():.2e} vs oracle")
         checked.append(layer)
-    result = run_cpu_baseline(wl, layers, repeats)
+    result = cpu_reference_baseline(wl, layers, workload_names)
     result["checked_layers"] = checked
+    result["openmp_port"] = openmp_port_baseline(wl, wl.num_layers, repeats)
 
     # The block bookkeeping of the same decode steps on the host: the
     # oracle's restatement of BlockManager, one Python call per op as the
@@ -988,11 +1152,130 @@ def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer) -> 
     return result
 
 
-def run_cpu_baseline(wl, layers: int, repeats: int) -> dict:
+def _host_cache(shape, dtype):
+    """A host cache tensor with every page touched (the values never
+    influence the data movement)."""
+    import torch
+
+    cache = torch.empty(shape, dtype=dtype)
+    cache.view(torch.int16 if cache.element_size() == 2 else torch.int32).fill_(0x3F80)
+    return cache
+
+
+def _median_seconds(fn, *, min_runs: int = 3, budget_s: float = 2.0) -> tuple[float, int]:
+    """Median wall time of ``fn`` over at least ``min_runs`` runs, more while
+    the budget lasts (one untimed run first)."""
+    fn()
+    times = []
+    spent = 0.0
+    while len(times) < min_runs or spent < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        spent += times[-1]
+        if len(times) >= 50:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_reference_baseline(wl, layers: int, workload_names) -> dict:
+    """The reference's own CPU path: the ``pytorch`` backend's torch ops
+    (index_copy_ store, index_select gather of whole blocks,
+    nanovllm/layers/paged_kv/pytorch_backend.py:26-50, with the validators
+    that check index values on host tensors, base.py:68-72) on host tensors,
+    driven as SDPAAttention drives them (one store per layer, one gather per
+    sequence and per K/V, attention.py:75-93, 284-300), with
+    torch.set_num_threads(the host cores this job may use).
+
+    The decode step is sampled: ``layers`` layers (each with its own new
+    rows) against ONE layer-sized host cache (the 28-layer cache does not fit
+    host memory), bytes counted as on the GPU; the per-layer time scales to
+    the 28-layer step.  The single-layer configurations are timed whole, each
+    operation as the median of at least 3 runs."""
+    import numpy as np
+    import torch
+
+    from nanokv import workloads
+    from nanokv.benchmark import TorchReferenceBackend, cpu_model, host_threads
+
+    threads = host_threads()
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    ref = TorchReferenceBackend()
+    try:
+        shape = (wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim)
+        kc, vc = _host_cache(shape, wl.dtype), _host_cache(shape, wl.dtype)
+        tables = torch.from_numpy(wl.padded_block_tables())
+        slots = torch.from_numpy(wl.slot_mapping)
+        lens = [int(n) for n in wl.num_tokens]
+
+        def layer(index: int) -> None:
+            ref.store(wl.key[index], wl.value[index], kc, vc, slots)
+            for i, n in enumerate(lens):
+                ref.gather(kc, tables[i], n)
+                ref.gather(vc, tables[i], n)
+
+        layer(0)
+        t0 = time.perf_counter()
+        for index in range(layers):
+            layer(index % wl.num_layers)
+        per_layer = (time.perf_counter() - t0) / layers
+        layer_bytes = wl.store_bytes(layers=1) + wl.gather_bytes(layers=1)
+        del kc, vc
+        configs = {}
+        for name in [n for n in workload_names if n]:
+            w = workloads.build(name)
+            wshape = (w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim)
+            wk, wv = _host_cache(wshape, w.dtype), _host_cache(wshape, w.dtype)
+            record = {}
+            if w.slot_mapping is not None:
+                wslots = torch.from_numpy(w.slot_mapping)
+                sec, runs = _median_seconds(lambda: ref.store(w.key, w.value, wk, wv, wslots))
+                nbytes = w.store_bytes(layers=1)
+                record["store"] = {"seconds": round(sec, 6), "runs": runs, "algorithmic_bytes": nbytes,
+                                   "gbps": round(nbytes / sec / 1e9, 3)}
+            if name != "decode_store":
+                wtables = torch.from_numpy(w.padded_block_tables())
+                wlens = [int(n) for n in w.context_lens]
+
+                def gathers():
+                    for i, n in enumerate(wlens):
+                        ref.gather(wk, wtables[i], n)
+                        ref.gather(wv, wtables[i], n)
+
+                sec, runs = _median_seconds(gathers)
+                nbytes = w.gather_bytes(layers=1)
+                record["gather_kv"] = {"seconds": round(sec, 6), "runs": runs, "algorithmic_bytes": nbytes,
+                                       "gbps": round(nbytes / sec / 1e9, 3)}
+            configs[name] = record
+            del wk, wv
+    finally:
+        torch.set_num_threads(previous)
+    return {
+        "value": round(layer_bytes / per_layer / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "ops": "reference pytorch backend torch ops: index_copy_ store, index_select gather "
+               "(nanovllm/layers/paged_kv/pytorch_backend.py:26-50), validators included",
+        "sample": (f"decode step: {layers} of the 28 layers (store of the 256 new rows, then 256 x 2 "
+                   f"per-sequence gathers of K and V) on host tensors, one layer-sized cache, "
+                   f"{per_layer:.2f} s per layer"),
+        "seconds_per_layer": round(per_layer, 4),
+        "decode_tokens_per_s_equivalent": round(wl.num_seqs / (per_layer * wl.num_layers), 3),
+        "torch_threads": threads,
+        "cpu_model": cpu_model(),
+        "configs": configs,
+    }
+
+
+def openmp_port_baseline(wl, layers: int, repeats: int) -> dict:
     """The oracle's C restatement (OpenMP) on the host cores: one decode
     step of ``layers`` layers (pack, then per layer store + K/V varlen
     gather) against ONE layer-sized host cache reused by every layer (the
-    full cache does not fit host memory), bytes counted as on the GPU."""
+    full cache does not fit host memory), bytes counted as on the GPU.  A
+    second CPU figure beside the reference's own torch ops."""
     import numpy as np
     import torch
 
@@ -1025,14 +1308,6 @@ def run_cpu_baseline(wl, layers: int, repeats: int) -> dict:
         times.append(time.perf_counter() - t0)
     seconds = sorted(times)[len(times) // 2]
     step_bytes = wl.store_bytes(layers=layers) + wl.gather_bytes(layers=layers)
-    model = "unknown"
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {
         "value": round(step_bytes / seconds / 1e9, 3),
         "unit": "GB/s",
@@ -1042,7 +1317,6 @@ def run_cpu_baseline(wl, layers: int, repeats: int) -> dict:
                    f"store + K/V varlen gather of the same decode step against one layer-sized "
                    f"host cache, median of {max(1, repeats)} runs, {seconds:.2f} s each"),
         "decode_tokens_per_s_equivalent": round(wl.num_seqs / (seconds * wl.num_layers / layers), 2),
-        "cpu_model": model,
     }
 
 

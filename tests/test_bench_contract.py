@@ -41,14 +41,54 @@ def test_algorithmic_bytes_closed_forms():
     assert wl.gather_bytes() == int(lens.sum()) * 4 * 2048 + 8 * blocks + 4 * 17
 
 
-def test_cpu_baseline_leg_runs_on_a_small_step():
+def test_cpu_baselines_run_on_a_small_step():
     sys.path.insert(0, str(REPO))
     import bench
 
     wl = workloads.build("decode_step", num_layers=2, num_live=8, churn=2, max_ctx=1024)
-    result = bench.run_cpu_baseline(wl, layers=2, repeats=1)
+    result = bench.cpu_reference_baseline(wl, 2, [])
     assert result["kind"] == "port" and result["unit"] == "GB/s"
-    assert result["value"] > 0 and result["cores"] >= 1
+    assert result["value"] > 0 and result["cores"] >= 1 and result["torch_threads"] == result["cores"]
+    assert "index_copy_" in result["ops"] and result["cpu_model"]
+    port = bench.openmp_port_baseline(wl, layers=2, repeats=1)
+    assert port["kind"] == "port" and port["value"] > 0
+
+
+def test_reference_torch_ops_on_host_equal_the_oracle():
+    """The CPU baseline times TorchReferenceBackend on host tensors; on the
+    same inputs it must compute what the oracle computes."""
+    import torch
+
+    from oracle import paged_kv as oracle
+
+    ref = benchmark.TorchReferenceBackend()
+    g = torch.Generator().manual_seed(3)
+    kc = torch.randn((6, 4, 2, 8), generator=g).to(torch.bfloat16)
+    vc = torch.randn((6, 4, 2, 8), generator=g).to(torch.bfloat16)
+    key = torch.randn((5, 2, 8), generator=g).to(torch.bfloat16)
+    value = torch.randn((5, 2, 8), generator=g).to(torch.bfloat16)
+    slots = torch.tensor([3, -1, 17, 0, 22], dtype=torch.int32)
+    hk, hv = kc.view(torch.int16).numpy().copy(), vc.view(torch.int16).numpy().copy()
+    oracle.store(key.view(torch.int16).numpy(), value.view(torch.int16).numpy(), hk, hv, slots.numpy())
+    ref.store(key, value, kc, vc, slots)
+    assert np.array_equal(kc.view(torch.int16).numpy(), hk)
+    assert np.array_equal(vc.view(torch.int16).numpy(), hv)
+    table = torch.tensor([5, 0, 2], dtype=torch.int32)
+    got = ref.gather(kc, table, 10).view(torch.int16).numpy()
+    assert np.array_equal(got, oracle.gather(hk, table.numpy(), 10))
+
+
+def test_environment_identity_fields():
+    identity = benchmark.environment_identity()
+    for key in ("timestamp_utc", "torch", "hip_status", "cpu_model", "host_threads", "platform"):
+        assert key in identity
+    assert identity["host_threads"] >= 1
+
+
+def test_bench_rejects_a_case_without_replay():
+    proc = subprocess.run([sys.executable, str(REPO / "bench.py"), "--case", "chunked_prefill"],
+                          capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 2 and "--profile-replay" in proc.stderr
 
 
 def test_bench_refuses_more_than_one_gpu():
