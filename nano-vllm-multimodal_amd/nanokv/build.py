@@ -28,6 +28,7 @@ SOURCES = (
     "nkv_prefill.hip",
     "nkv_pool.hip",
     "nkv_noalloc.hip",
+    "nkv_store_gather.hip",
 )
 OFFLOAD_ARCH = "gfx950"
 HIPCC_FLAGS = (

@@ -177,6 +177,87 @@ class HIPPagedKVBackend:
         )
 
 
+    def build_store_gather_plan(
+        self,
+        cache: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_q: torch.Tensor,
+        cu_seqlens_k: torch.Tensor,
+        num_tokens: int,
+        total_tokens: int,
+    ) -> torch.Tensor:
+        """Plan of :meth:`store_gather` for one prefill step (valid for every
+        layer's caches of the shape and dtype of ``cache``): each new
+        token's context row and table-derived slot, and the chunks of every
+        request's cached prefix.  ``num_tokens`` is the step's new-token
+        count (rows of K/V and of slot_mapping, cu_seqlens_q[-1]) and
+        ``total_tokens`` its context rows (cu_seqlens_k[-1]); the plan is
+        laid out for them."""
+        self._load()
+        num_blocks, block_size, heads, head_dim = cache.shape
+        writer_map, tag = self._writer_map(cache.device, num_blocks)
+        return ops.build_store_gather_plan(
+            block_tables, cu_seqlens_q, cu_seqlens_k, writer_map, tag, num_tokens, total_tokens,
+            num_blocks, block_size, heads * head_dim, cache.dtype,
+        )
+
+    def _writer_map(self, device: torch.device, num_blocks: int) -> tuple[torch.Tensor, int]:
+        """The block -> writing request map of store_gather plans for caches
+        of ``num_blocks`` blocks on ``device`` (one int64 per block, zeroed
+        on creation), and the next step tag for it."""
+        key = (str(device), int(num_blocks))
+        with _LOAD_LOCK:
+            maps = self.__dict__.setdefault("_writer_maps", {})
+            entry = maps.get(key)
+            if entry is None or entry[1] >= 2**32 - 1:
+                entry = [torch.zeros(max(1, int(num_blocks)), dtype=torch.int64, device=device), 0]
+                maps[key] = entry
+            entry[1] += 1
+            return entry[0], entry[1]
+
+    def store_gather(
+        self,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        key_cache: torch.Tensor,
+        value_cache: torch.Tensor,
+        slot_mapping: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_q: torch.Tensor,
+        cu_seqlens_k: torch.Tensor,
+        total_tokens: int,
+        *,
+        plan: torch.Tensor | None = None,
+        out: tuple[torch.Tensor, torch.Tensor] | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """The prefill step's store followed by the gather of every
+        request's whole context (attention.py:87-93 then :250-259), in one
+        launch: the caches end as :meth:`store` leaves them and the outputs
+        equal :meth:`gather_varlen` over ``cu_seqlens_k`` afterwards.  Exact
+        when no slot repeats and each token's slot is -1 or the slot of its
+        own position in its request's block table, as prefill packing
+        produces.  ``plan`` from :meth:`build_store_gather_plan` (one per
+        step, built for these token and context counts) skips the planning
+        launch; ``out`` reuses output buffers."""
+        validate_store_inputs(key, value, key_cache, value_cache, slot_mapping)
+        validate_varlen_inputs(key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens)
+        if (cu_seqlens_q.dtype != torch.int32 or cu_seqlens_q.ndim != 1
+                or cu_seqlens_q.numel() != cu_seqlens_k.numel()):
+            raise ValueError("cu_seqlens_q must be int32 with one entry per request plus one")
+        self._load()
+        if plan is None:
+            plan = self.build_store_gather_plan(key_cache, block_tables, cu_seqlens_q, cu_seqlens_k,
+                                                key.shape[0], total_tokens)
+        if out is None:
+            key_out = torch.empty((total_tokens, *key_cache.shape[2:]), dtype=key_cache.dtype,
+                                  device=key_cache.device)
+            out = (key_out, torch.empty_like(key_out))
+        if out[0].shape[0] != total_tokens or out[1].shape != out[0].shape:
+            raise ValueError("store+gather outputs must hold total_tokens rows")
+        ops.store_gather(key, value, key_cache, value_cache, slot_mapping, plan,
+                         block_tables.shape[0], out[0], out[1])
+        return out
+
     def build_attention_plan(
         self,
         cache: torch.Tensor,

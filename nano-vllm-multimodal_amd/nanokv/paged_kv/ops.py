@@ -26,6 +26,14 @@ too, paged_kv_cuda.cu:168-171).  Additive ops, with no reference schema:
                            Tensor block_tables, Tensor plan,
                            Tensor first_part, float scale,
                            Tensor(a!) out) -> ()
+    build_store_gather_plan(Tensor block_tables, Tensor cu_seqlens_q,
+                            Tensor cu_seqlens_k, Tensor(a!) writer_map,
+                            int step_tag, int num_tokens, int total_tokens,
+                            int num_blocks, int block_size, int row_elems,
+                            ScalarType dtype) -> Tensor
+    store_gather(Tensor key, Tensor value, Tensor(a!) key_cache,
+                 Tensor(b!) value_cache, Tensor slot_mapping, Tensor plan,
+                 int num_seqs, Tensor(c!) key_out, Tensor(d!) value_out) -> ()
 
 Every kernel runs on the current stream of the tensors' device and returns
 before it completes, like the reference ops.
@@ -56,6 +64,13 @@ SCHEMAS = {
     "paged_attention_decode": "paged_attention_decode(Tensor q, Tensor key_cache, "
     "Tensor value_cache, Tensor block_tables, Tensor plan, Tensor first_part, float scale, "
     "Tensor(a!) out) -> ()",
+    "build_store_gather_plan": "build_store_gather_plan(Tensor block_tables, "
+    "Tensor cu_seqlens_q, Tensor cu_seqlens_k, Tensor(a!) writer_map, int step_tag, "
+    "int num_tokens, int total_tokens, int num_blocks, int block_size, int row_elems, "
+    "ScalarType dtype) -> Tensor",
+    "store_gather": "store_gather(Tensor key, Tensor value, Tensor(a!) key_cache, "
+    "Tensor(b!) value_cache, Tensor slot_mapping, Tensor plan, int num_seqs, "
+    "Tensor(c!) key_out, Tensor(d!) value_out) -> ()",
     "build_prefill_plan": "build_prefill_plan(Tensor cu_seqlens_q, Tensor cu_seqlens_k, "
     "int total_q_tokens, int group) -> Tensor",
     "paged_attention_prefill": "paged_attention_prefill(Tensor q, Tensor key_cache, "
@@ -250,6 +265,62 @@ def _gather_varlen_impl(key_cache, value_cache, block_tables, cu_seqlens_k, tota
     return key_out, value_out
 
 
+def _build_store_gather_plan_impl(
+    block_tables, cu_seqlens_q, cu_seqlens_k, writer_map, step_tag: int, num_tokens: int,
+    total_tokens: int, num_blocks: int, block_size: int, row_elems: int, dtype: torch.dtype,
+) -> torch.Tensor:
+    device = _require_device("paged KV HIP store+gather plan", block_tables, cu_seqlens_q,
+                             cu_seqlens_k, writer_map)
+    if writer_map.dtype != torch.int64 or not writer_map.is_contiguous():
+        raise ValueError("writer_map must be a contiguous int64 tensor")
+    if not 0 < step_tag < 2**32:
+        raise ValueError("step_tag must be in [1, 2**32)")
+    num_seqs = _require_cu("cu_seqlens_q", cu_seqlens_q)
+    _require_cu("cu_seqlens_k", cu_seqlens_k, num_seqs)
+    if block_tables.dtype != torch.int32 or block_tables.ndim != 2 or not block_tables.is_contiguous():
+        raise ValueError("block_tables must be a contiguous two-dimensional int32 tensor")
+    code = dtype_code(dtype)
+    library = _lib.load_library()
+    nbytes = int(library.nkv_store_gather_plan_bytes(num_tokens, total_tokens, num_seqs,
+                                                     block_size, row_elems, code))
+    plan = torch.empty(max(nbytes, 16) // 4, dtype=torch.int32, device=device)
+    status = library.nkv_build_store_gather_plan(
+        block_tables.data_ptr(), block_tables.shape[1], cu_seqlens_q.data_ptr(),
+        cu_seqlens_k.data_ptr(), num_seqs, num_tokens, total_tokens, block_size, row_elems,
+        num_blocks, code, writer_map.data_ptr(), writer_map.numel() * 8, step_tag,
+        plan.data_ptr(), plan.numel() * 4, _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::build_store_gather_plan")
+    return plan
+
+
+def _store_gather_impl(key, value, key_cache, value_cache, slot_mapping, plan, num_seqs: int,
+                       key_out, value_out) -> None:
+    device = _require_device("paged KV HIP store+gather", key, value, key_cache, value_cache,
+                             slot_mapping, plan, key_out, value_out)
+    _require_contiguous_cache("paged KV HIP store+gather", key_cache, value_cache)
+    if len({t.dtype for t in (key, value, key_cache, value_cache, key_out, value_out)}) != 1:
+        raise RuntimeError("Paged KV HIP store+gather dtype mismatch")
+    if not (key_out.is_contiguous() and value_out.is_contiguous()):
+        raise ValueError("store+gather outputs must be contiguous")
+    if key_out.shape != value_out.shape or key_out.shape[1:] != key_cache.shape[2:]:
+        raise ValueError("store+gather outputs must be [rows, kv_heads, head_dim] of the caches")
+    if plan.dtype != torch.int32 or plan.ndim != 1 or not plan.is_contiguous():
+        raise ValueError("store+gather plan must be a contiguous 1-D int32 tensor")
+    if key.shape[1] > 1 and key.stride(1) != key.shape[2]:
+        key = key.contiguous()
+    if value.shape[1] > 1 and value.stride(1) != value.shape[2]:
+        value = value.contiguous()
+    num_blocks, block_size, heads, head_dim = key_cache.shape
+    status = _lib.load_library().nkv_store_gather(
+        key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+        slot_mapping.data_ptr(), key.shape[0], key.stride(0), value.stride(0), plan.data_ptr(),
+        plan.numel() * 4, num_seqs, key_out.shape[0], block_size, heads * head_dim, num_blocks,
+        dtype_code(key.dtype), key_out.data_ptr(), value_out.data_ptr(), _stream(device),
+    )
+    _lib.check(status, "nanovllm_paged_kv::store_gather")
+
+
 def _build_attention_plan_impl(cu_seqlens_k, total_tokens: int, block_size: int):
     device = _require_device("paged KV HIP attention plan", cu_seqlens_k)
     if cu_seqlens_k.dtype != torch.int32 or cu_seqlens_k.ndim != 1 or not cu_seqlens_k.is_contiguous():
@@ -400,6 +471,8 @@ def register_ops() -> None:
         fragment.impl("gather_varlen_planned", _gather_planned_impl, "CUDA")
         fragment.impl("build_attention_plan", _build_attention_plan_impl, "CUDA")
         fragment.impl("paged_attention_decode", _paged_attention_decode_impl, "CUDA")
+        fragment.impl("build_store_gather_plan", _build_store_gather_plan_impl, "CUDA")
+        fragment.impl("store_gather", _store_gather_impl, "CUDA")
         fragment.impl("build_prefill_plan", _build_prefill_plan_impl, "CUDA")
         fragment.impl("paged_attention_prefill", _paged_attention_prefill_impl, "CUDA")
         _FRAGMENT = fragment
@@ -417,3 +490,5 @@ build_attention_plan = _build_attention_plan_impl
 paged_attention_decode = _paged_attention_decode_impl
 build_prefill_plan = _build_prefill_plan_impl
 paged_attention_prefill = _paged_attention_prefill_impl
+build_store_gather_plan = _build_store_gather_plan_impl
+store_gather = _store_gather_impl
