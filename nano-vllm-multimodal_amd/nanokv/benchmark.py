@@ -268,6 +268,18 @@ class PreparedWorkload:
             self.algorithmic_bytes["gather_varlen_kv"] = wl.gather_bytes(layers=1)
             self.reference_bytes["gather_varlen_kv"] = 2 * effective_bytes(
                 "gather", self.total, wl.num_kv_heads, wl.head_dim, element)
+        if wl.phase == "prefill" and wl.slot_mapping is not None:
+            # the same step's store and context gather as one launch
+            self.cu_q = torch.from_numpy(wl.cu_seqlens_q()).to(self.device)
+            self.sg_plan = backend.build_store_gather_plan(
+                self.key_cache, self.tables, self.cu_q, self.cu, self.key.shape[0], self.total)
+            self.sg_out = (torch.empty_like(self.k_out), torch.empty_like(self.v_out))
+            self.ops["store_gather"] = lambda: backend.store_gather(
+                self.key, self.value, self.key_cache, self.value_cache, self.slots, self.tables,
+                self.cu_q, self.cu, self.total, plan=self.sg_plan, out=self.sg_out)
+            self.algorithmic_bytes["store_gather"] = wl.store_gather_bytes(layers=1)
+            self.reference_bytes["store_gather"] = (self.reference_bytes["store"]
+                                                    + self.reference_bytes["gather_varlen_kv"])
 
     def steady_state_us(self, op: str, rotations: int = 16, rounds: int = 4) -> float:
         """Microseconds per launch of ``op`` launched back to back, rotating
@@ -292,6 +304,21 @@ class PreparedWorkload:
                 key, value = self.key.clone(), self.value.clone()
                 calls.append(lambda key=key, value=value, d_slots=d_slots: backend.store(
                     key, value, self.key_cache, self.value_cache, d_slots))
+            elif op == "store_gather":
+                slots = self.wl.slot_mapping.astype(np.int64)
+                moved = np.where(slots >= 0, ((slots // bs + k * shift) % nb) * bs + slots % bs, -1)
+                d_slots = torch.from_numpy(moved.astype(np.int32)).to(self.device)
+                base = self.wl.padded_block_tables().astype(np.int64)
+                tables = torch.from_numpy(np.where(base >= 0, (base + k * shift) % nb, -1)
+                                          .astype(np.int32)).to(self.device)
+                plan = backend.build_store_gather_plan(self.key_cache, tables, self.cu_q, self.cu,
+                                                       self.key.shape[0], self.total)
+                key, value = self.key.clone(), self.value.clone()
+                out = (torch.empty_like(self.k_out), torch.empty_like(self.v_out))
+                calls.append(lambda key=key, value=value, d_slots=d_slots, tables=tables, plan=plan,
+                             out=out: backend.store_gather(
+                                 key, value, self.key_cache, self.value_cache, d_slots, tables,
+                                 self.cu_q, self.cu, self.total, plan=plan, out=out))
             elif op == "gather_varlen_kv":
                 base = self.wl.padded_block_tables().astype(np.int64)
                 tables = torch.from_numpy(np.where(base >= 0, (base + k * shift) % nb, -1)
@@ -338,6 +365,21 @@ class PreparedWorkload:
                     if not torch.equal(got, ref.gather(cache, table, n).view(words)):
                         raise AssertionError(f"{self.name}: hip gather of sequence {i} differs from "
                                              f"the reference backend")
+        if "store_gather" in self.ops:
+            # the store is idempotent: after it the fused op must leave the
+            # same caches and give the reference's gathers of them
+            self.ops["store_gather"]()
+            if not (torch.equal(self.key_cache.view(words), expect_k.view(words))
+                    and torch.equal(self.value_cache.view(words), expect_v.view(words))):
+                raise AssertionError(f"{self.name}: hip store+gather leaves other caches")
+            starts = self.wl.cu_seqlens_k().tolist()
+            for i, n in enumerate(self.context_lens.tolist()):
+                table = self.tables[i, : max(1, -(-n // self.wl.block_size))]
+                for cache, out in ((expect_k, self.sg_out[0]), (expect_v, self.sg_out[1])):
+                    got = out[starts[i]:starts[i] + n].view(words)
+                    if not torch.equal(got, ref.gather(cache, table, n).view(words)):
+                        raise AssertionError(f"{self.name}: hip store+gather of sequence {i} "
+                                             f"differs from the reference backend")
         torch.cuda.synchronize(self.device)
 
 
@@ -397,6 +439,11 @@ def run_workload(name: str, *, iterations: int = 50, warmup: int = 5, device=Non
                _time_with_flush(prepared.ops["gather_varlen_kv"], flush, iterations, warmup),
                prepared.reference_bytes["gather_varlen_kv"])
         steady("gather_varlen_kv")
+        if "store_gather" in prepared.ops:
+            record("store_gather", prepared.algorithmic_bytes["store_gather"],
+                   _time_with_flush(prepared.ops["store_gather"], flush, iterations, warmup),
+                   prepared.reference_bytes["store_gather"])
+            steady("store_gather")
         record("build_gather_plan", 0, _time_with_flush(
             lambda: prepared.backend.build_gather_plan(prepared.key_cache, prepared.tables,
                                                        prepared.cu, prepared.total),

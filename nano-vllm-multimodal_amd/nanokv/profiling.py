@@ -344,6 +344,8 @@ def algorithmic_bytes_for(case: str) -> dict[str, int]:
         found["store_rows_kernel"] = wl.store_bytes(layers=1)
     if case != "decode_store":
         found["gather_planned_kernel"] = wl.gather_bytes(layers=1)
+    if case in ("chunked_prefill", "narrow_rows"):
+        found["store_gather_kernel"] = wl.store_gather_bytes(layers=1)
     return found
 
 

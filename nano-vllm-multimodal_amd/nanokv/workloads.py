@@ -121,6 +121,21 @@ class Workload:
         return layers * (int(lens.sum()) * 4 * self.row_bytes + 8 * blocks + 4 * (self.num_seqs + 1))
 
 
+    def cu_seqlens_q(self) -> np.ndarray:
+        """Exclusive scan of the new tokens per sequence (prefill)."""
+        return np.concatenate([[0], np.cumsum(self.num_scheduled.astype(np.int64))]).astype(np.int32)
+
+    def store_gather_bytes(self, layers: int | None = None) -> int:
+        """The fused prefill store + context gather: the store's and the
+        gather's bytes, less the new rows the gather would read back from the
+        cache (the fused launch writes them to the output from the K/V row it
+        already read)."""
+        layers = self.num_layers if layers is None else layers
+        new_rows = int((self.slot_mapping >= 0).sum())
+        return (self.store_bytes(layers=layers) + self.gather_bytes(layers=layers)
+                - layers * new_rows * 2 * self.row_bytes)
+
+
 def _generator(seed: int) -> torch.Generator:
     g = torch.Generator()
     g.manual_seed(seed)

@@ -148,6 +148,9 @@ def test_algorithmic_bytes_follow_the_workloads():
     c2 = profiling.algorithmic_bytes_for("chunked_prefill")
     wl = workloads.build("chunked_prefill")
     assert c2 == {"store_rows_kernel": wl.store_bytes(layers=1),
-                  "gather_planned_kernel": wl.gather_bytes(layers=1)}
+                  "gather_planned_kernel": wl.gather_bytes(layers=1),
+                  "store_gather_kernel": wl.store_gather_bytes(layers=1)}
+    # the fused launch skips reading the 8192 new rows back (K and V, 2 KiB each)
+    assert c2["store_gather_kernel"] == c2["store_rows_kernel"] + c2["gather_planned_kernel"] - 8192 * 2 * 2048
     assert set(profiling.algorithmic_bytes_for("decode_store")) == {"store_rows_kernel"}
     assert set(profiling.algorithmic_bytes_for("prefix_gather")) == {"gather_planned_kernel"}
