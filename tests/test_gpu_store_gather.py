@@ -228,3 +228,73 @@ def test_empty_step_and_context_only(backend, gpu_device):
         torch.from_numpy(table).to(gpu_device), torch.zeros(3, dtype=torch.int32, device=gpu_device),
         torch.zeros(3, dtype=torch.int32, device=gpu_device), 0)
     assert k_out.shape == (0, 2, 64) and v_out.shape == (0, 2, 64)
+
+
+def _expected_plan(tables, cu_q, cu_k, bs, chunk, num_blocks):
+    """The plan restated on the host: per token {output row, slot of its
+    position}; per cached chunk {source row, output row, rows, request} and
+    {token of the chunk's first row, [lo, hi) rows written in this step}."""
+    num_seqs = len(cu_q) - 1
+    meta, writer = [], {}
+    for t in range(int(cu_q[-1])):
+        i = int(np.searchsorted(cu_q, t, side="right")) - 1
+        lk, lq = int(cu_k[i + 1] - cu_k[i]), int(cu_q[i + 1] - cu_q[i])
+        p = lk - lq + t - int(cu_q[i])
+        block = int(tables[i, p // bs]) if p // bs < tables.shape[1] else -1
+        slot = block * bs + p % bs if 0 <= block < num_blocks else -1
+        meta.append((int(cu_k[i]) + p, slot))
+        if slot >= 0 and (p % bs == 0 or t == cu_q[i]):
+            writer[block] = (i, p // bs)
+    entries = []
+    for i in range(num_seqs):
+        cached = int(cu_k[i + 1] - cu_k[i]) - int(cu_q[i + 1] - cu_q[i])
+        for row0 in range(0, max(cached, 0), chunk):
+            rows = min(chunk, cached - row0)
+            block = int(tables[i, row0 // bs]) if row0 // bs < tables.shape[1] else -1
+            src = block * bs + row0 % bs if 0 <= block < num_blocks else -1
+            tail = (0, 0, 0, 0)
+            if src >= 0 and block in writer:
+                w, wl = writer[block]
+                wlk = int(cu_k[w + 1] - cu_k[w])
+                wstart = wlk - int(cu_q[w + 1] - cu_q[w])
+                first = wl * bs + row0 % bs
+                lo = max(0, min(rows, wstart - first))
+                hi = max(lo, min(rows, wlk - first))
+                if lo < hi:
+                    tail = (int(cu_q[w]) + first - wstart, lo, hi, 0)
+            entries.append((src, int(cu_k[i]) + row0, rows, i) + tail)
+    return meta, entries
+
+
+@pytest.mark.parametrize("source", ["narrow_rows", "random"])
+def test_plan_marks_rows_written_in_the_step(backend, gpu_device, source):
+    """The plan, read back, equals its host restatement: every cached chunk
+    whose rows another request writes in this step names that token range
+    (the fused launch takes those rows from K/V, never from the cache)."""
+    from nanokv import _lib, workloads
+
+    if source == "narrow_rows":
+        wl = workloads.build("narrow_rows")
+        tables, cu_q, cu_k = wl.padded_block_tables(), wl.cu_seqlens_q(), wl.cu_seqlens_k()
+        bs, nb, heads, dim = wl.block_size, wl.num_blocks, wl.num_kv_heads, wl.head_dim
+    else:
+        rng = np.random.default_rng(31)
+        bs, nb, heads, dim = 16, 3000, 2, 128
+        tables, _, cu_q, cu_k = _prefill_batch(rng, 31, bs, nb)
+    cache = torch.empty((nb, bs, heads, dim), dtype=torch.bfloat16, device=gpu_device)
+    t, total = int(cu_q[-1]), int(cu_k[-1])
+    plan = backend.build_store_gather_plan(
+        cache, torch.from_numpy(tables).to(gpu_device), torch.from_numpy(cu_q).to(gpu_device),
+        torch.from_numpy(cu_k).to(gpu_device), t, total).cpu().numpy()
+    chunk = _lib.load_library().nkv_gather_plan_rows(bs, heads * dim, _lib.NKV_DTYPE_BFLOAT16)
+    meta, entries = _expected_plan(tables, cu_q, cu_k, bs, chunk, nb)
+    meta_words = (t * 8 + 15) // 16 * 4
+    np.testing.assert_array_equal(plan[:2 * t].reshape(t, 2), np.asarray(meta, np.int32).reshape(t, 2))
+    got = plan[meta_words:].reshape(-1, 8)
+    assert len(entries) <= got.shape[0]
+    np.testing.assert_array_equal(got[:len(entries)], np.asarray(entries, np.int32).reshape(-1, 8))
+    assert (got[len(entries):] == 0).all()
+    written = sum(1 for e in entries if e[6] > e[5])
+    print(f"[store_gather plan {source}] {len(entries)} cached chunks, {written} with rows written "
+          f"in the step", flush=True)
+    assert written > 0
