@@ -413,6 +413,11 @@ def main(argv=None) -> int:
             f"{step_ms:.3f} ms step")
     profiled = profiled_median(PROFILE_FILE, "gather_planned_kernel", gather_launch_bytes)
 
+    fused_step = measure_fused_step(wl, device, backend, packer, batch, cache, new_k, new_v, total,
+                                    k_out, v_out, args.steps, args.warmup)
+    log(f"[bench] fused store+gather step: {fused_step['ms_per_step']:.3f} ms/step "
+        f"({fused_step['gbps']:.0f} GB/s of its own bytes)")
+
     copy_reference = measure_copy_reference(wl, device, backend, packer, cache, total, k_out, v_out,
                                             args.steps)
     log(f"[bench] copy reference: torch copy_ {copy_reference['torch_copy_gbps']:.0f} GB/s, "
@@ -566,6 +571,7 @@ def main(argv=None) -> int:
             "step_ms_store_attention": round(attn_step_ms, 4),
             "decode_tokens_per_s_store_attention": round(B / (attn_step_ms * 1e-3), 2),
         },
+        "fused_store_gather_step": fused_step,
         "copy_reference": copy_reference,
         "other_workloads": other_workloads,
         "prefill_attention": prefill_attention,
@@ -785,6 +791,67 @@ def measure_other_workloads(device, iterations: int) -> list[dict]:
             })
         torch.cuda.empty_cache()
     return records
+
+
+def measure_fused_step(wl, device, backend, packer, batch, cache, new_k, new_v, total, k_out, v_out,
+                       steps: int, warmup: int) -> dict:
+    """The same decode step with each layer's store and gather as one fused
+    launch (nkv_store_gather: each sequence's one new token is the last row
+    of its context, read once and written to the cache and the output).
+    Layer 0's outputs are first compared bit-exactly with the separate
+    store-then-gather path's.  Bytes are the fused launch's own: the store's
+    and the gather's, less the new rows the gather would read back."""
+    import torch
+
+    B, L = wl.num_seqs, wl.num_layers
+    cu_q = torch.arange(B + 1, dtype=torch.int32, device=device)
+    ctx = packer.pack_decode(batch)
+    plan = backend.build_gather_plan(cache[0, 0], ctx.block_tables, ctx.cu_seqlens_k, total)
+    backend.store(new_k[0], new_v[0], cache[0, 0], cache[1, 0], ctx.slot_mapping)
+    backend.gather_varlen(cache[0, 0], cache[1, 0], ctx.block_tables, ctx.cu_seqlens_k, total,
+                          plan=plan, out=(k_out, v_out))
+    fk, fv = torch.empty_like(k_out), torch.empty_like(v_out)
+
+    def step(out=(fk, fv)):
+        c = packer.pack_decode(batch)
+        sg_plan = backend.build_store_gather_plan(cache[0, 0], c.block_tables, cu_q, c.cu_seqlens_k,
+                                                  B, total)
+        for layer in range(L):
+            backend.store_gather(new_k[layer], new_v[layer], cache[0, layer], cache[1, layer],
+                                 c.slot_mapping, c.block_tables, cu_q, c.cu_seqlens_k, total,
+                                 plan=sg_plan, out=out)
+
+    step()
+    torch.cuda.synchronize()
+    # layers > 0 overwrote fk/fv; redo layer 0 alone for the comparison
+    c = packer.pack_decode(batch)
+    sg_plan = backend.build_store_gather_plan(cache[0, 0], c.block_tables, cu_q, c.cu_seqlens_k, B, total)
+    backend.store_gather(new_k[0], new_v[0], cache[0, 0], cache[1, 0], c.slot_mapping, c.block_tables,
+                         cu_q, c.cu_seqlens_k, total, plan=sg_plan, out=(fk, fv))
+    torch.cuda.synchronize()
+    if not (torch.equal(fk.view(torch.int16), k_out.view(torch.int16))
+            and torch.equal(fv.view(torch.int16), v_out.view(torch.int16))):
+        raise AssertionError("fused store+gather differs from store then gather on layer 0")
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    step_bytes = L * (wl.store_bytes(layers=1) + wl.gather_bytes(layers=1)
+                      - int((wl.slot_mapping >= 0).sum()) * 2 * wl.row_bytes)
+    return {
+        "what": "pack + store+gather plan + 28 x nkv_store_gather (one launch per layer); "
+                "layer 0 bit-identical to store then gather",
+        "ms_per_step": round(ms, 4),
+        "decode_tokens_per_s": round(B / (ms * 1e-3), 2),
+        "algorithmic_bytes_per_step": step_bytes,
+        "gbps": round(step_bytes / (ms * 1e-3) / 1e9, 2),
+    }
 
 
 def measure_copy_reference(wl, device, backend, packer, cache, total, k_out, v_out, reps: int) -> dict:
