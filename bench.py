@@ -51,7 +51,8 @@ METRIC = "paged KV store+gather GB/s (fraction of HBM peak); decode-step tokens/
 # configurations, the full decode step (store + gather) and the decode step
 # with paged-attention decode in place of the gather.
 PROFILE_CASES = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows", "decode_step",
-                 "decode_attention")
+                 "decode_attention", "grouped_decode_2x8", "grouped_decode_4x7", "grouped_decode_8x4",
+                 "prefill_attention", "block_pool")
 
 
 PROFILE_FILE = REPO_ROOT / "profiles" / "decode_step_rocprof.json"
@@ -181,6 +182,34 @@ def main(argv=None) -> int:
 
         replay_workload(args.case, args.profile_replay, device)
         print(f"profile replay complete: {args.case} x {args.profile_replay}", flush=True)
+        return 0
+    if args.case in GROUPED_CASES:
+        from nanokv import workloads
+
+        hkv, group = GROUPED_CASES[args.case]
+        case = grouped_decode_setup(device, backend, workloads.build("decode_step", num_layers=1),
+                                    hkv, group, torch.Generator(device=device).manual_seed(29))
+        check_decode_attention(backend, case, sample=6)
+        for _ in range(args.profile_replay):
+            case["call"]()
+        torch.cuda.synchronize(device)
+        print(f"profile replay complete: {args.case} x {args.profile_replay}", flush=True)
+        return 0
+    if args.case == "block_pool":
+        from nanokv import workloads
+        from nanokv.packing import DevicePacker
+
+        replay_block_pool(workloads.build("decode_step", num_layers=1), device,
+                          DevicePacker(device, workloads.BLOCK_SIZE), args.profile_replay)
+        print(f"profile replay complete: block_pool x {args.profile_replay}", flush=True)
+        return 0
+    if args.case == "prefill_attention":
+        case = prefill_setup(device, backend)
+        check_prefill_attention(backend, case)
+        for _ in range(args.profile_replay):
+            case["call"]()
+        torch.cuda.synchronize(device)
+        print(f"profile replay complete: prefill_attention x {args.profile_replay}", flush=True)
         return 0
     if args.prefill_only:
         print(json.dumps(measure_prefill_attention(device, backend, args.steps)), flush=True)
@@ -597,23 +626,23 @@ GROUPED_LAYOUTS = (
 )
 
 
-def measure_grouped_decode(device, backend, wl, reps: int) -> list[dict]:
-    """Paged-attention decode of one layer over the decode step's 256
-    contexts (block 256, blocks placed at random) for the grouped-query
-    layouts above: G = 7 and 8 run on the MFMA kernel, as does G = 4.  One
-    event pair on the current stream around `reps` calls (partials + merge);
-    bytes = the K and V rows read once, plus q and out."""
+GROUPED_CASES = {"grouped_decode_2x8": (2, 8), "grouped_decode_4x7": (4, 7),
+                 "grouped_decode_8x4": (8, 4)}
+
+
+def grouped_decode_setup(device, backend, wl, hkv: int, group: int, gen) -> dict:
+    """One decode-attention layer over the decode step's 256 contexts (block
+    256, blocks placed at random by ``gen``) with ``hkv`` kv heads and
+    ``group`` query heads per kv head: caches, tables, q, plan and the call.
+    Bytes = the K and V rows read once, plus q and out."""
     import numpy as np
     import torch
-
-    from nanokv.benchmark import MI355X_HBM_PEAK_GBPS
 
     lens = np.asarray(wl.num_tokens, dtype=np.int64)
     bs = wl.block_size
     need = -(-lens // bs)
     nb = int(need.sum()) + 8
     total = int(lens.sum())
-    gen = torch.Generator(device=device).manual_seed(29)
     perm = torch.randperm(nb, device=device, generator=gen).to(torch.int32)
     tables = torch.full((lens.size, int(need.max())), -1, dtype=torch.int32, device=device)
     cursor = 0
@@ -621,38 +650,87 @@ def measure_grouped_decode(device, backend, wl, reps: int) -> list[dict]:
         tables[i, :n] = perm[cursor:cursor + n]
         cursor += n
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=device)
+    kc = torch.empty((nb, bs, hkv, 128), dtype=torch.bfloat16, device=device).normal_(generator=gen)
+    vc = torch.empty_like(kc).normal_(generator=gen)
+    q = torch.randn((lens.size, hkv * group, 128), device=device, generator=gen).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    plan = backend.build_attention_plan(kc, cu, total)
+    scale = 1.0 / math.sqrt(128)
+
+    def call():
+        backend.paged_attention_decode(q, kc, vc, tables, cu, total, scale, plan=plan, out=out)
+
+    return {"call": call, "q": q, "kc": kc, "vc": vc, "tables": tables, "lens": lens, "out": out,
+            "scale": scale, "bytes": total * hkv * 128 * 2 * 2 + 2 * q.numel() * 2}
+
+
+def host_attention(q, k, v, scale: float, offset: int | None = None):
+    """float32 softmax(scale q K^T) V on the host for one request: q [Lq,
+    Hq, D], k / v [Lk, Hkv, D]; query head h reads kv head h // (Hq / Hkv);
+    with ``offset``, query j sees keys [0, offset + j] (bottom-right causal)."""
+    import torch
+
+    group = q.shape[1] // k.shape[1]
+    keys = k.float().cpu().repeat_interleave(group, dim=1).transpose(0, 1)      # [Hq, Lk, D]
+    values = v.float().cpu().repeat_interleave(group, dim=1).transpose(0, 1)
+    queries = q.float().cpu().transpose(0, 1)                                    # [Hq, Lq, D]
+    scores = torch.matmul(queries, keys.transpose(1, 2).contiguous()) * scale    # [Hq, Lq, Lk]
+    if offset is not None:
+        lq, lk = q.shape[0], k.shape[0]
+        visible = torch.arange(lk)[None, :] <= (torch.arange(lq) + offset)[:, None]
+        scores = scores.masked_fill(~visible[None], float("-inf"))
+    return torch.matmul(torch.softmax(scores, dim=-1), values).transpose(0, 1)   # [Lq, Hq, D]
+
+
+def check_decode_attention(backend, case: dict, sample: int = 6) -> None:
+    """The decode attention of ``sample`` sequences against host_attention
+    over their K/V rows gathered bit-exactly, within 1e-3 + 1e-2 |ref|."""
+    import numpy as np
+    import torch
+
+    case["call"]()
+    torch.cuda.synchronize()
+    for i in np.linspace(0, len(case["lens"]) - 1, sample).astype(int).tolist():
+        n = int(case["lens"][i])
+        table = case["tables"][i, : -(-n // case["kc"].shape[1])].contiguous()
+        expect = host_attention(case["q"][i:i + 1], backend.gather(case["kc"], table, n),
+                                backend.gather(case["vc"], table, n), case["scale"])[0]
+        err = (case["out"][i].float().cpu() - expect).abs()
+        if bool((err > 1e-3 + 1e-2 * expect.abs()).any()):
+            raise AssertionError(f"decode attention, sequence {i}: max error {float(err.max()):.3e}")
+
+
+def measure_grouped_decode(device, backend, wl, reps: int) -> list[dict]:
+    """Paged-attention decode of one layer over the decode step's 256
+    contexts for the grouped-query layouts above (the MFMA decode kernel).
+    One event pair on the current stream around `reps` calls (partials +
+    merge)."""
+    import torch
+
+    from nanokv.benchmark import MI355X_HBM_PEAK_GBPS
+
+    gen = torch.Generator(device=device).manual_seed(29)
     records = []
     for name, hkv, g in GROUPED_LAYOUTS:
-        kc = torch.empty((nb, bs, hkv, 128), dtype=torch.bfloat16, device=device)
-        kc.normal_(generator=gen)
-        vc = torch.empty_like(kc).normal_(generator=gen)
-        q = torch.randn((lens.size, hkv * g, 128), device=device, generator=gen).to(torch.bfloat16)
-        out = torch.empty_like(q)
-        plan = backend.build_attention_plan(kc, cu, total)
-        scale = 1.0 / math.sqrt(128)
-
-        def call():
-            backend.paged_attention_decode(q, kc, vc, tables, cu, total, scale, plan=plan, out=out)
-
+        case = grouped_decode_setup(device, backend, wl, hkv, g, gen)
         for _ in range(3):
-            call()
+            case["call"]()
         torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(reps):
-            call()
+            case["call"]()
         end.record()
         torch.cuda.synchronize()
         us = start.elapsed_time(end) * 1e3 / reps
-        nbytes = total * hkv * 128 * 2 * 2 + 2 * q.numel() * 2
-        achieved = nbytes / (us * 1e-6) / 1e9
+        achieved = case["bytes"] / (us * 1e-6) / 1e9
         records.append({
             "layout": name, "kv_heads": hkv, "q_heads_per_kv_head": g,
             "kernel": "attn_decode_mfma_kernel" if g >= 3 else "attn_decode_partial_kernel",
-            "us": round(us, 2), "algorithmic_bytes": nbytes, "achieved": round(achieved, 1),
+            "us": round(us, 2), "algorithmic_bytes": case["bytes"], "achieved": round(achieved, 1),
             "unit": "GB/s", "frac": round(achieved / MI355X_HBM_PEAK_GBPS, 4),
         })
-        del kc, vc
+        del case
         torch.cuda.empty_cache()
     return records
 
@@ -672,18 +750,13 @@ def chunked_prefill_shape(seed: int = 17):
     return q_lens.tolist(), (q_lens + cached).tolist()
 
 
-def measure_prefill_attention(device, backend, reps: int) -> dict:
-    """Causal prefill attention read straight from the paged cache (the
-    Flash path's prefill call) on the chunked-prefill step: Qwen3-VL-2B's 16
-    query heads over 8 kv heads, 256-row blocks.  Algorithmic FLOPs = 4 x
-    head_dim x query heads x the (query, visible key) pairs.  Beside it, the
-    reference's SDPA prefill on the same GPU: per request, the
-    pytorch-backend gathers of K and V and SDPA with the prefix-causal mask
-    (nanovllm/layers/attention.py:226-282)."""
+def prefill_setup(device, backend) -> dict:
+    """The chunked-prefill step's paged prefill attention: Qwen3-VL-2B's 16
+    query heads over 8 kv heads, 256-row blocks placed at random; caches,
+    tables, q, plan and the call.  Algorithmic FLOPs = 4 x head_dim x query
+    heads x the (query, visible key) pairs."""
     import numpy as np
     import torch
-
-    from nanokv.benchmark import LaunchTimer
 
     q_lens, k_lens = chunked_prefill_shape()
     hkv, g, bs, dim = 8, 2, 256, 128
@@ -704,14 +777,58 @@ def measure_prefill_attention(device, backend, reps: int) -> dict:
     scale = 1.0 / math.sqrt(dim)
     plan = backend.build_prefill_plan(q, kc, cu_q, cu_k)
     out = torch.empty_like(q)
-    stream = torch.cuda.current_stream(device)
-    timer = LaunchTimer(stream)
 
-    def launch():
+    def call():
         backend.paged_attention_prefill(q, kc, vc, tables, cu_q, cu_k, scale, plan=plan, out=out)
 
+    pairs = sum(sum(lk - lq + j + 1 for j in range(lq)) for lq, lk in zip(q_lens, k_lens))
+    return {"call": call, "q": q, "kc": kc, "vc": vc, "tables": tables, "cu_q": cu_q, "cu_k": cu_k,
+            "q_lens": q_lens, "k_lens": k_lens, "scale": scale, "out": out,
+            "flops": 4 * dim * hkv * g * pairs, "dims": (hkv, g, dim)}
+
+
+def check_prefill_attention(backend, case: dict, requests: int = 2) -> None:
+    """The prefill attention of the ``requests`` shortest requests against
+    host_attention (bottom-right causal) over their K/V rows gathered
+    bit-exactly, within 1e-3 + 2^-7 (|ref| + the same attention over |V|):
+    twice the bound of the parity tests, whose terms are the bf16 weights,
+    the output rounding and accumulation order."""
+    import torch
+
+    case["call"]()
+    torch.cuda.synchronize()
+    starts = case["cu_q"].cpu().tolist()
+    order = sorted(range(len(case["q_lens"])), key=lambda i: case["k_lens"][i])[:requests]
+    for i in order:
+        lq, lk = case["q_lens"][i], case["k_lens"][i]
+        table = case["tables"][i, : -(-lk // case["kc"].shape[1])].contiguous()
+        k = backend.gather(case["kc"], table, lk)
+        v = backend.gather(case["vc"], table, lk)
+        q = case["q"][starts[i]:starts[i] + lq]
+        expect = host_attention(q, k, v, case["scale"], offset=lk - lq)
+        ref_abs = host_attention(q, k, v.abs(), case["scale"], offset=lk - lq)
+        err = (case["out"][starts[i]:starts[i] + lq].float().cpu() - expect).abs()
+        if bool((err > 1e-3 + 2.0 ** -7 * (expect.abs() + ref_abs)).any()):
+            raise AssertionError(f"prefill attention, request {i}: max error {float(err.max()):.3e}")
+
+
+def measure_prefill_attention(device, backend, reps: int) -> dict:
+    """Causal prefill attention read straight from the paged cache (the
+    Flash path's prefill call) on the chunked-prefill step
+    (:func:`prefill_setup`).  Beside it, the reference's SDPA prefill on the
+    same GPU: per request, the pytorch-backend gathers of K and V and SDPA
+    with the prefix-causal mask (nanovllm/layers/attention.py:226-282)."""
+    import torch
+
+    from nanokv.benchmark import LaunchTimer
+
+    case = prefill_setup(device, backend)
+    q_lens, k_lens, q, kc, vc, tables = (case[k] for k in ("q_lens", "k_lens", "q", "kc", "vc", "tables"))
+    cu_q, scale, flops = case["cu_q"], case["scale"], case["flops"]
+    stream = torch.cuda.current_stream(device)
+    timer = LaunchTimer(stream)
     for _ in range(3):
-        launch()
+        case["call"]()
     torch.cuda.synchronize()
     # One event pair around back-to-back launches: the host enqueues a call
     # faster than the kernel runs, so the stream never idles and the mean is
@@ -719,11 +836,9 @@ def measure_prefill_attention(device, backend, reps: int) -> dict:
     # idle stream waits for the host's next call).
     t0 = timer.start()
     for _ in range(reps):
-        launch()
+        case["call"]()
     timer.stop(t0)
     us = timer.durations_us()[0] / reps
-    pairs = sum(sum(lk - lq + j + 1 for j in range(lq)) for lq, lk in zip(q_lens, k_lens))
-    flops = 4 * dim * hkv * g * pairs
     ref = reference_backend()
 
     def sdpa_path():
@@ -953,6 +1068,41 @@ def block_pool_steps(wl, seed: int = 11):
             free_blocks -= n
             lens[slot] = int(n_tokens)
         yield ops, dict(lens)
+
+
+def replay_block_pool(wl, device, packer, steps: int) -> None:
+    """The profiling replay of the block pool: the admission of the decode
+    step's sequences, then ``steps`` scheduler steps (each flushed to the
+    device pool and packed from it), with no events.  Checked: no op failed,
+    and the pool's free count equals its blocks less those the steps hold
+    (block_pool_steps tracks them exactly; no block is shared)."""
+    import torch
+
+    from nanokv.pool import DeviceBlockPool
+
+    width = -(-(16384 + 4 * steps + 1) // wl.block_size) + 1
+    pool = DeviceBlockPool(wl.num_blocks, wl.block_size, max_seqs=2 * wl.num_seqs,
+                           max_blocks_per_seq=width, device=device)
+    held = 0
+    for k, (ops, lens) in enumerate(block_pool_steps(wl)):
+        if k > steps:
+            break
+        for op in ops:
+            if op[0] == "append":
+                pool.append(op[1])
+            elif op[0] == "deallocate":
+                pool.deallocate(op[1])
+            else:
+                pool.allocate(op[1], op[2])
+        pool.flush()
+        slots = sorted(lens)
+        packer.pack_decode_pool(pool, slots, [lens[s] for s in slots])
+        held = sum(-(-n // wl.block_size) for n in lens.values())
+    torch.cuda.synchronize(device)
+    pool.check()
+    live = int(pool.meta[2].item())
+    if live != wl.num_blocks - held:
+        raise AssertionError(f"block pool holds {wl.num_blocks - live} blocks, the steps {held}")
 
 
 def measure_block_pool(wl, device, packer, batch, steps: int, warmup: int) -> dict:

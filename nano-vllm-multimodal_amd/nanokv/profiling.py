@@ -45,7 +45,10 @@ from typing import Iterable, Sequence
 
 HBM_PEAK_GBPS = 8000.0
 CASES = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows", "decode_step",
-         "decode_attention")
+         "decode_attention", "grouped_decode_2x8", "grouped_decode_4x7", "grouped_decode_8x4",
+         "prefill_attention", "block_pool")
+GROUPED = {"grouped_decode_2x8": (2, 8), "grouped_decode_4x7": (4, 7), "grouped_decode_8x4": (8, 4)}
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 COPY_CALIBRATION_MIB = 1024
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
@@ -243,7 +246,8 @@ def _find_csv(directory: Path, suffix: str) -> Path:
 
 
 def summarize(case: str, out: Path, algorithmic_bytes: dict[str, int], *,
-              commands: dict[str, list[str]] | None = None, skip_first: int = 1) -> dict:
+              commands: dict[str, list[str]] | None = None, skip_first: int = 1,
+              algorithmic_flops: dict[str, int] | None = None) -> dict:
     """One case's figures from the five passes under ``out``: per kernel the
     trace statistics, the achieved bandwidth on its median duration
     (algorithmic bytes per launch from ``algorithmic_bytes``, keyed by a
@@ -268,6 +272,12 @@ def summarize(case: str, out: Path, algorithmic_bytes: dict[str, int], *,
             record["algorithmic_bytes"] = nbytes
             record["achieved_gbps_at_median"] = nbytes / (stats["median_us"] * 1e3)
             record["hbm_fraction_at_median"] = record["achieved_gbps_at_median"] / HBM_PEAK_GBPS
+        flops = next((f for prefix, f in (algorithmic_flops or {}).items() if name.startswith(prefix)),
+                     None)
+        if flops:
+            record["algorithmic_flops"] = flops
+            record["achieved_tflops_at_median"] = flops / (stats["median_us"] * 1e6)
+            record["mfma_fraction_at_median"] = record["achieved_tflops_at_median"] / MFMA_BF16_PEAK_TFLOPS
         moved = {}
         for counter, per_kernel in traffic.items():
             if name in per_kernel:
@@ -310,6 +320,14 @@ def render_markdown(summary: dict, title: str | None = None) -> str:
             f"{k['p05_us']:.2f}–{k['p95_us']:.2f} | "
             + (f"{k['algorithmic_bytes']:,} | {gbps:,.0f} | {100 * gbps / summary['peak_gbps']:.1f}% |"
                if gbps else "— | — | — |"))
+    mfma = {n: k for n, k in summary["kernels"].items() if "achieved_tflops_at_median" in k}
+    if mfma:
+        lines += ["", f"MFMA-bound kernels against the dense bf16 peak of {MFMA_BF16_PEAK_TFLOPS:,.0f} "
+                      "TFLOP/s:", "", "| Kernel | Algorithmic FLOPs | TFLOP/s at median | % of peak |",
+                  "|---|---:|---:|---:|"]
+        for name, k in mfma.items():
+            lines.append(f"| `{name}` | {k['algorithmic_flops']:,} | {k['achieved_tflops_at_median']:.1f} | "
+                         f"{100 * k['mfma_fraction_at_median']:.1f}% |")
     if summary["counter_factors"]:
         f = summary["counter_factors"]
         lines += ["", "## HBM traffic (FETCH_SIZE / WRITE_SIZE)", "",
@@ -328,6 +346,25 @@ def render_markdown(summary: dict, title: str | None = None) -> str:
     return "\n".join(lines) + "\n"
 
 
+def algorithmic_flops_for(case: str) -> dict[str, int]:
+    """Algorithmic FLOPs per launch of the case's MFMA-bound kernels: the
+    chunked-prefill step's causal attention, 4 x head_dim x query heads x
+    the (query, visible key) pairs of 16 requests (query lengths scaled to
+    8,192 tokens, 8 continuing after 1-4 cached 256-row blocks, seed 17)."""
+    if case != "prefill_attention":
+        return {}
+    import numpy as np
+
+    rng = np.random.default_rng(17)
+    raw = rng.integers(128, 4097, 16).astype(np.float64)
+    q_lens = np.floor(raw / raw.sum() * 8192).astype(np.int64)
+    q_lens[-1] += 8192 - q_lens.sum()
+    cached = np.zeros(16, np.int64)
+    cached[:8] = rng.integers(1, 5, 8) * 256
+    pairs = int(sum(lq * (lq + 1) // 2 + lq * c for lq, c in zip(q_lens.tolist(), cached.tolist())))
+    return {"attn_prefill_kernel": 4 * 128 * 16 * pairs}
+
+
 def algorithmic_bytes_for(case: str) -> dict[str, int]:
     """Algorithmic bytes per launch of the case's kernels (the workload's
     own byte counts), keyed by short-name prefix."""
@@ -338,6 +375,14 @@ def algorithmic_bytes_for(case: str) -> dict[str, int]:
         total = int(wl.num_tokens.sum())
         q_bytes = wl.num_seqs * 16 * wl.head_dim * 2
         return {"attn_decode_partial_kernel": total * wl.row_bytes * 2 + 2 * q_bytes}
+    if case in GROUPED:
+        hkv, group = GROUPED[case]
+        wl = workloads.build("decode_step", num_layers=1)
+        total = int(wl.num_tokens.sum())
+        q_bytes = wl.num_seqs * hkv * group * 128 * 2
+        return {"attn_decode_mfma_kernel": total * hkv * 128 * 2 * 2 + 2 * q_bytes}
+    if case in ("prefill_attention", "block_pool"):
+        return {}
     wl = workloads.build(case, num_layers=1) if case == "decode_step" else workloads.build(case)
     found = {}
     if wl.slot_mapping is not None:
@@ -381,7 +426,8 @@ def main(argv: Sequence[str] | None = None) -> int:
         return 0
     recorded = args.out / "commands.json"
     commands = json.loads(recorded.read_text()) if recorded.is_file() else dict(plan)
-    summary = summarize(args.case, args.out, algorithmic_bytes_for(args.case), commands=commands)
+    summary = summarize(args.case, args.out, algorithmic_bytes_for(args.case), commands=commands,
+                        algorithmic_flops=algorithmic_flops_for(args.case))
     stem = args.name or f"{args.case}_rocprof"
     args.profiles.mkdir(parents=True, exist_ok=True)
     (args.profiles / f"{stem}.json").write_text(json.dumps(summary, indent=1) + "\n")

@@ -298,3 +298,36 @@ def test_plan_marks_rows_written_in_the_step(backend, gpu_device, source):
     print(f"[store_gather plan {source}] {len(entries)} cached chunks, {written} with rows written "
           f"in the step", flush=True)
     assert written > 0
+
+
+def test_decode_step_shape(backend, gpu_device):
+    """One new token per sequence (the decode step through the fused op):
+    256 contexts log-uniform in [256, 16384] at full size, then a small
+    batch whose last rows are graph-bucket padding as the decode graph's
+    replay fill leaves them (model_runner.py:993-1011): a token with slot -1
+    and context length 0, so it is neither stored nor gathered."""
+    from nanokv import workloads
+
+    wl = workloads.build("decode_step", num_layers=1)
+    shape = (wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim)
+    g = torch.Generator(device=gpu_device).manual_seed(8)
+    kc = torch.empty(shape, dtype=wl.dtype, device=gpu_device)
+    kc.view(torch.int16).random_(-32768, 32767, generator=g)
+    vc = torch.empty_like(kc)
+    vc.view(torch.int16).random_(-32768, 32767, generator=g)
+    cu_q = np.arange(wl.num_seqs + 1, dtype=np.int32)
+    print(f"[store_gather decode] seqs={wl.num_seqs} rows={int(wl.num_tokens.sum())}", flush=True)
+    _run_and_check(backend, gpu_device, kc, vc, wl.key[0].to(gpu_device), wl.value[0].to(gpu_device),
+                   wl.padded_block_tables(), wl.slot_mapping, cu_q, wl.cu_seqlens_k())
+
+    bs, nb = 16, 64
+    kc = torch.randn(nb, bs, 2, 64, device=gpu_device, generator=g).to(torch.float16)
+    vc = torch.randn_like(kc)
+    table = np.array([[5, 9, -1], [11, -1, -1], [-1, -1, -1], [-1, -1, -1]], np.int32)
+    lens = np.array([20, 3, 0, 0])                      # the last two are padding rows
+    slots = np.array([9 * bs + 3, 11 * bs + 2, -1, -1], np.int32)
+    cu_q = np.arange(5, dtype=np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    key = torch.randn(4, 2, 64, device=gpu_device, generator=g).to(torch.float16)
+    value = torch.randn_like(key)
+    _run_and_check(backend, gpu_device, kc, vc, key, value, table, slots, cu_q, cu_k)

@@ -154,3 +154,20 @@ def test_algorithmic_bytes_follow_the_workloads():
     assert c2["store_gather_kernel"] == c2["store_rows_kernel"] + c2["gather_planned_kernel"] - 8192 * 2 * 2048
     assert set(profiling.algorithmic_bytes_for("decode_store")) == {"store_rows_kernel"}
     assert set(profiling.algorithmic_bytes_for("prefix_gather")) == {"gather_planned_kernel"}
+
+
+def test_prefill_flops_match_the_bench_workload():
+    import sys
+
+    sys.path.insert(0, str(profiling.Path(__file__).resolve().parents[1]))
+    import bench
+
+    q_lens, k_lens = bench.chunked_prefill_shape()
+    pairs = sum(sum(lk - lq + j + 1 for j in range(lq)) for lq, lk in zip(q_lens, k_lens))
+    assert profiling.algorithmic_flops_for("prefill_attention") == {"attn_prefill_kernel": 4 * 128 * 16 * pairs}
+    # 2 kv heads x 128 dims of K and V per context row, plus q and out of 16 query heads
+    from nanokv import workloads
+
+    total = int(workloads.build("decode_step", num_layers=1).num_tokens.sum())
+    assert profiling.algorithmic_bytes_for("grouped_decode_2x8") == {
+        "attn_decode_mfma_kernel": total * 2 * 128 * 2 * 2 + 2 * 256 * 16 * 128 * 2}
