@@ -589,3 +589,43 @@ def test_decode_step_full_size_two_layers(backend, gpu_device):
         ctables = _remap_tables(tables, remap)
         np.testing.assert_array_equal(words(k_out), c_oracle.gather_varlen(hk, ctables, cu, threads=8))
         np.testing.assert_array_equal(words(v_out), c_oracle.gather_varlen(hv, ctables, cu, threads=8))
+
+
+def test_store_gather_above_4gib_offsets(backend, gpu_device):
+    """Rows past 4 GiB into a cache (8192 blocks of 256 rows of 2 KiB per
+    cache, 4 GiB each): the store's, the gather's and the fused
+    store+gather's byte offsets need 64 bits there."""
+    nb, bs, heads, dim = 8192, 256, 8, 128
+    kc = torch.zeros((nb, bs, heads, dim), dtype=torch.bfloat16, device=gpu_device)
+    vc = torch.zeros_like(kc)
+    top = np.arange(nb - 3, nb, dtype=np.int32)                 # the last three blocks
+    rng = np.random.default_rng(4)
+    slots = np.concatenate([top[2] * bs + np.arange(bs - 40, bs), top[0] * bs + rng.permutation(bs)[:30]])
+    slots = slots.astype(np.int32)
+    slots[[3, 17]] = -1
+    g = torch.Generator(device=gpu_device).manual_seed(6)
+    key = torch.randn((slots.size, heads, dim), device=gpu_device, generator=g).to(torch.bfloat16)
+    value = torch.randn_like(key)
+    backend.store(key, value, kc, vc, torch.from_numpy(slots).to(gpu_device))
+    hk = np.zeros((3, bs, heads, dim), np.int16)
+    hv = np.zeros_like(hk)
+    local = np.where(slots >= 0, (slots // bs - (nb - 3)) * bs + slots % bs, -1).astype(np.int32)
+    oracle.store(words(key), words(value), hk, hv, local)
+    np.testing.assert_array_equal(words(kc[nb - 3:]), hk)
+    np.testing.assert_array_equal(words(vc[nb - 3:]), hv)
+    table = torch.tensor([nb - 1, nb - 3, nb - 2], dtype=torch.int32, device=gpu_device)
+    length = 2 * bs + 77
+    np.testing.assert_array_equal(words(backend.gather(kc, table, length)),
+                                  oracle.gather(hk, np.array([2, 0, 1]), length))
+    # the fused op on one request whose new rows are the last 40 of block nb-1
+    cu_q = torch.tensor([0, 40], dtype=torch.int32, device=gpu_device)
+    cu_k = torch.tensor([0, bs], dtype=torch.int32, device=gpu_device)
+    tables = torch.tensor([[nb - 1]], dtype=torch.int32, device=gpu_device)
+    new_k = torch.randn((40, heads, dim), device=gpu_device, generator=g).to(torch.bfloat16)
+    new_v = torch.randn_like(new_k)
+    fused_slots = torch.from_numpy(((nb - 1) * bs + np.arange(bs - 40, bs)).astype(np.int32)).to(gpu_device)
+    k_out, v_out = backend.store_gather(new_k, new_v, kc, vc, fused_slots, tables, cu_q, cu_k, bs)
+    oracle.store(words(new_k), words(new_v), hk, hv, (2 * bs + np.arange(bs - 40, bs)).astype(np.int32))
+    np.testing.assert_array_equal(words(k_out), oracle.gather(hk, np.array([2]), bs))
+    np.testing.assert_array_equal(words(v_out), oracle.gather(hv, np.array([2]), bs))
+    np.testing.assert_array_equal(words(kc[nb - 3:]), hk)
