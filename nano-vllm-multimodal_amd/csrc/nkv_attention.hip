@@ -579,8 +579,18 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
   typedef typename E::X4 X4;
   __shared__ DecShared sh;
 
+  // The kv head rotates with the entry.  Workgroups are dealt to the 8 XCDs
+  // round-robin (blockIdx % 8), so head blockIdx % Hkv would pin each XCD to
+  // one byte offset inside every cache row; some offsets stream slower than
+  // others on MI355X, and the XCD pinned to the slowest ends the launch late
+  // (8 kv heads x G = 4: XCDs done after 504-601 us pinned, 556-567 us
+  // rotated).  Workgroups of one XCD with the same blockIdx % Hkv are
+  // `period` entries apart, so adding part / period walks them over every
+  // head; for a fixed entry the heads stay a permutation.
   const int64_t part = blockIdx.x / num_kv_heads;
-  const int32_t kh = static_cast<int32_t>(blockIdx.x % num_kv_heads);
+  const int32_t period = 8 / min(8, num_kv_heads & -num_kv_heads);  // 8 / gcd(Hkv, 8)
+  const int32_t kh =
+      static_cast<int32_t>((blockIdx.x % num_kv_heads + part / period) % num_kv_heads);
   const int4 entry = plan[part];
   const int32_t row0 = entry.x;
   const int32_t seq = entry.z;

@@ -180,6 +180,36 @@ def test_long_contexts_over_small_blocks(backend, gpu_device, hkv, g, bs):
     check_close(out, ref, f"hkv={hkv} g={g} bs={bs}")
 
 
+def expected_attention_plan(lens, rows):
+    """The decode plan restated: sequence by sequence, entries of `rows`
+    context rows in row order (the last one short when rows does not divide
+    the length), {row0, rows, seq, 0}; first part of each sequence."""
+    first = np.concatenate([[0], np.cumsum([-(-n // rows) for n in lens])]).astype(np.int64)
+    entries = [(r, min(rows, n - r), i, 0) for i, n in enumerate(lens) for r in range(0, n, rows)]
+    return np.array(entries, dtype=np.int64).reshape(-1, 4), first
+
+
+def test_plan_at_the_sequence_limit(backend, gpu_device):
+    """NKV_MAX_PLAN_SEQS (8192) sequences, lengths 0 .. 3000 over 16-row
+    blocks (entries of 768 rows): the plan kernel's LDS scan at its largest;
+    the whole plan equals the restatement, padding entries empty."""
+    from nanokv import _lib
+
+    rng = np.random.default_rng(81)
+    lens = rng.integers(0, 3001, 8192)
+    lens[:7] = [0, 768, 769, 767, 1, 1536, 0]
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).to(gpu_device)
+    cache = torch.empty((1, 16, 1, 128), dtype=torch.bfloat16, device=gpu_device)
+    rows = int(_lib.load_library().nkv_attention_entry_rows(16))
+    assert rows == 768
+    plan, first = backend.build_attention_plan(cache, cu, int(lens.sum()))
+    expect, expect_first = expected_attention_plan(lens.tolist(), rows)
+    got = plan.cpu().numpy().astype(np.int64)
+    np.testing.assert_array_equal(first.cpu().numpy(), expect_first)
+    np.testing.assert_array_equal(got[: len(expect)], expect)
+    assert not got[len(expect):].any()
+
+
 @pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
 def test_invalid_block_ids_drop_their_rows(backend, gpu_device, hkv, g):
     """A block id outside [0, num_blocks) (or -1) inside a context drops that
