@@ -223,6 +223,44 @@ __global__ __launch_bounds__(kPlanThreads) void attn_plan_kernel(
   }
 }
 
+// Cache row of each context row [row0, row0 + nrows) of sequence seq, -1
+// where the block id is missing from the table or outside the cache.  The
+// table is read once per block, not once per row: the entry's block ids go
+// to `blocks` (LDS, at least nrows ints: every block of the entry holds one
+// of its rows) in one round of loads, and the rows are expanded from them
+// with no further memory access.  A per-row loop of table loads waits for
+// each load before the next (768 rows over 256 threads were three loads in
+// a row, about 1.5 us each under load).  Ends with `rows` visible to the
+// whole workgroup; `blocks` may be reused after it.
+template <int NT>
+__device__ __forceinline__ void resolve_rows(const int32_t* __restrict__ tables,
+                                             int64_t table_stride, int32_t seq, int32_t row0,
+                                             int32_t nrows, int32_t block_size,
+                                             int32_t num_blocks, int32_t* blocks,
+                                             int32_t* rows) {
+  const int32_t first = row0 / block_size;
+  const int32_t nblk =
+      nrows > 0 ? static_cast<int32_t>((static_cast<int64_t>(row0) + nrows - 1) / block_size) -
+                      first + 1
+                : 0;
+  for (int32_t b = threadIdx.x; b < nblk; b += NT) {
+    const int64_t logical = static_cast<int64_t>(first) + b;
+    int32_t block = -1;
+    if (logical < table_stride) {
+      block = tables[static_cast<int64_t>(seq) * table_stride + logical];
+      if (block < 0 || block >= num_blocks) block = -1;
+    }
+    blocks[b] = block;
+  }
+  __syncthreads();  // block ids in LDS
+  for (int32_t t = threadIdx.x; t < nrows; t += NT) {
+    const int64_t ctx = static_cast<int64_t>(row0) + t;
+    const int32_t block = blocks[ctx / block_size - first];
+    rows[t] = block >= 0 ? block * block_size + static_cast<int32_t>(ctx % block_size) : -1;
+  }
+  __syncthreads();  // rows resolved
+}
+
 // Stores one (entry, query head) partial: the wave's lanes hold dims
 // 2 lane, 2 lane + 1 of the unnormalised output (a0, a1) against reference
 // max mm with weight sum lsum.  The sums go out as fp16 pairs scaled by
@@ -297,20 +335,7 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
   const int head0 = HKV >= 4 ? slot : slot % HKV;
   const int row_off = HKV >= 4 ? 0 : slot / HKV;
 
-  // Cache row of every context row of the entry, -1 where the block id is
-  // missing from the table or outside the cache.
-  for (int32_t t = threadIdx.x; t < nrows; t += kAttnThreads) {
-    const int32_t ctx = row0 + t;
-    const int32_t logical = ctx / block_size;
-    int32_t cache_row = -1;
-    if (logical < table_stride) {
-      const int32_t block = tables[static_cast<int64_t>(seq) * table_stride + logical];
-      if (block >= 0 && block < num_blocks) cache_row = block * block_size + ctx % block_size;
-    }
-    sh.rows[t] = cache_row;
-  }
-  __syncthreads();  // rows resolved before any wave reads them
-
+  // q first, so its loads overlap the block-id loads of the rows below.
   u32x4 qf[NC][G];
   const uint16_t* qs = q + static_cast<int64_t>(seq) * q_seq_stride;
 #pragma unroll
@@ -321,6 +346,12 @@ __global__ __launch_bounds__(kAttnThreads) NKV_ATTN_OCCUPANCY void attn_decode_p
       qf[c][g] = *reinterpret_cast<const u32x4*>(qs + qh * kHeadDim + sub * 8);
     }
   }
+
+  // Cache row of every context row of the entry; the block ids pass through
+  // the merge buffer, which is idle until the loop below ends.
+  static_assert(sizeof(sh.acc) >= kEntryRows * sizeof(int32_t), "block-id scratch too small");
+  resolve_rows<kAttnThreads>(tables, table_stride, seq, row0, nrows, block_size, num_blocks,
+                             reinterpret_cast<int32_t*>(&sh.acc[0][0][0]), sh.rows);
 
   float m[NC][G], l[NC][G], acc[NC][G][8];
 #pragma unroll
@@ -605,19 +636,9 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
 
-  for (int32_t t = tid; t < nrows; t += kDecThreads) {
-    const int32_t ctx = row0 + t;
-    const int32_t logical = ctx / block_size;
-    int32_t cache_row = -1;
-    if (logical < table_stride) {
-      const int32_t block = tables[static_cast<int64_t>(seq) * table_stride + logical];
-      if (block >= 0 && block < num_blocks) cache_row = block * block_size + ctx % block_size;
-    }
-    sh.rows[t] = cache_row;
-  }
-
   // Q^T operands (B of S^T = K Q^T): lane holds head c16 of this kv head,
-  // dims 32 dc + 8 g4 .. +8; zero for padding columns.
+  // dims 32 dc + 8 g4 .. +8; zero for padding columns.  Loaded first, so
+  // they overlap the block-id loads of the rows.
   X8 qb[4];
   {
     const bool col_ok = c16 < group;
@@ -630,8 +651,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
       qb[dc] = __builtin_bit_cast(X8, v);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // q and the block ids have landed (nothing else in flight)
-  __syncthreads();                // rows resolved
+  // The block ids pass through wave 0's ring, which no copy fills before
+  // the rows are resolved.
+  static_assert(sizeof(sh.wave[0].ring) >= kEntryRows * sizeof(int32_t),
+                "block-id scratch too small");
+  resolve_rows<kDecThreads>(tables, table_stride, seq, row0, nrows, block_size, num_blocks,
+                            reinterpret_cast<int32_t*>(&sh.wave[0].ring), sh.rows);
+  __builtin_amdgcn_s_waitcnt(0);  // q has landed: only the chunk copies are in flight below
 
   const uint32_t row_bytes = static_cast<uint32_t>(num_kv_heads) * kHeadBytes;
   const uint8_t* const k_head = key_cache + static_cast<int64_t>(kh) * kHeadBytes;

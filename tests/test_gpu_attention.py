@@ -191,8 +191,9 @@ def expected_attention_plan(lens, rows):
 
 def test_plan_at_the_sequence_limit(backend, gpu_device):
     """NKV_MAX_PLAN_SEQS (8192) sequences, lengths 0 .. 3000 over 16-row
-    blocks (entries of 768 rows): the plan kernel's LDS scan at its largest;
-    the whole plan equals the restatement, padding entries empty."""
+    blocks (entries of nkv_attention_entry_rows(16) rows, 768 by default):
+    the plan kernel's LDS scan at its largest; the whole plan equals the
+    restatement, padding entries empty."""
     from nanokv import _lib
 
     rng = np.random.default_rng(81)
@@ -201,7 +202,6 @@ def test_plan_at_the_sequence_limit(backend, gpu_device):
     cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).to(gpu_device)
     cache = torch.empty((1, 16, 1, 128), dtype=torch.bfloat16, device=gpu_device)
     rows = int(_lib.load_library().nkv_attention_entry_rows(16))
-    assert rows == 768
     plan, first = backend.build_attention_plan(cache, cu, int(lens.sum()))
     expect, expect_first = expected_attention_plan(lens.tolist(), rows)
     got = plan.cpu().numpy().astype(np.int64)
