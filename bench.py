@@ -13,9 +13,13 @@ bf16), 256 live sequences with contexts log-uniform in [256, 16384] after
 Prints one JSON line:  value = store+gather algorithmic GB/s of the step
 (sum of the bytes the store and gather must move / step time), plus
 decode tokens/s, the HBM roofline of the dominant kernel (the varlen
-gather, timed live with events on its stream) and a CPU baseline (the
-oracle's C restatement on the host cores, bounded sample; the same leg
-checks the GPU outputs of --check-layers against the oracle).  A second
+gather, timed live with events on its stream) and a CPU baseline: the
+reference pytorch backend's torch ops (index_copy_ store, index_select
+gather) on host tensors with every host thread, over the same step and the
+single-layer configurations, with the oracle's OpenMP C restatement timed
+beside it as a second figure.  The same leg first checks the GPU outputs
+of --check-layers against the oracle (store+gather bit-exact, attention
+within tolerance).  A second
 timed step replaces the gather by its consumer, paged-attention decode read
 straight from the cache (16 query heads), reported under "attention", and
 "block_pool" times the same steps' block bookkeeping replayed on the device
