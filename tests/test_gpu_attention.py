@@ -210,6 +210,21 @@ def test_plan_at_the_sequence_limit(backend, gpu_device):
     assert not got[len(expect):].any()
 
 
+@pytest.mark.parametrize("hkv,g", [(3, 4), (5, 3), (6, 4)])
+def test_head_rotation_over_many_entries(backend, gpu_device, hkv, g):
+    """The MFMA kernel rotates the kv head with the plan entry (period
+    8 / gcd(Hkv, 8): 8 for 3 and 5 kv heads, 4 for 6), so each of the 8
+    XCDs walks every head; over 40 sequences of up to three 768-row entries
+    every (entry, head) pair must still be computed exactly once."""
+    rng = np.random.default_rng(hkv * 10 + g)
+    lens = rng.integers(1, 3 * 768 + 1, 40).tolist()
+    dev, host, total = build_case(gpu_device, hkv, g, 16, lens, seed=hkv * 31 + g)
+    scale = 1.0 / math.sqrt(128)
+    out = backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev["tables"], dev["cu"],
+                                         total, scale)
+    check_close(out, reference(host, scale), f"rotation hkv={hkv} g={g}")
+
+
 @pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
 def test_invalid_block_ids_drop_their_rows(backend, gpu_device, hkv, g):
     """A block id outside [0, num_blocks) (or -1) inside a context drops that
