@@ -321,8 +321,9 @@ def main(argv=None) -> int:
             query = q[i].float().cpu().unsqueeze(-1)
             weights = torch.softmax(torch.matmul(keys, query).squeeze(-1) * softmax_scale, dim=-1)
             expect = torch.matmul(weights.unsqueeze(1), values).squeeze(1)
+            expect_abs = torch.matmul(weights.unsqueeze(1), values.abs()).squeeze(1)
             err = (attn_out[i].float().cpu() - expect).abs()
-            if bool((err > 1e-3 + 1e-2 * expect.abs()).any()):
+            if bool((err > attention_tolerance(expect, expect_abs)).any()):
                 raise AssertionError(f"decode attention, sequence {i}: max error {float(err.max()):.3e}")
 
     if args.case == "decode_step":
@@ -397,11 +398,12 @@ def main(argv=None) -> int:
     attn_us = attn_timer.durations_us()
     # per call at the rate it runs inside the step: back to back over the
     # 28 layers' caches, one event pair around them
+    # (the plan built once per step, as an engine builds it)
     actx = packer.pack_decode(batch)
-    aplan = backend.build_attention_plan(cache[0, 0], actx.cu_seqlens_k, total)
     torch.cuda.synchronize()
     start_evt.record(stream)
     for _ in range(args.steps):
+        aplan = backend.build_attention_plan(cache[0, 0], actx.cu_seqlens_k, total)
         for layer in range(L):
             backend.paged_attention_decode(q, cache[0, layer], cache[1, layer], actx.block_tables,
                                            actx.cu_seqlens_k, total, softmax_scale, plan=aplan,
@@ -409,19 +411,22 @@ def main(argv=None) -> int:
     end_evt.record(stream)
     torch.cuda.synchronize()
     attn_mean = start_evt.elapsed_time(end_evt) * 1e3 / (args.steps * L)
-    # The flash_attn_with_kvcache drop-in on the same contexts: it takes only
-    # the lengths tensor, so it sizes its plan for the tables' full width
-    # (no host read of the lengths).
+    # The flash_attn_with_kvcache drop-in on the same contexts.  It takes only
+    # the lengths tensor: the first call of a step reads the context total
+    # back and builds the plan, which the step's other layers reuse; each
+    # step here passes a new lengths tensor, as an engine's step does.
     from nanokv.flash import flash_attn_with_kvcache
 
     q4 = q.unsqueeze(1)
-    flash_attn_with_kvcache(q4, cache[0, 0], cache[1, 0], cache_seqlens=actx.context_lens,
+    flash_attn_with_kvcache(q4, cache[0, 0], cache[1, 0], cache_seqlens=actx.context_lens.clone(),
                             block_table=actx.block_tables, softmax_scale=softmax_scale, causal=True)
     torch.cuda.synchronize()
+    step_lengths = [actx.context_lens.clone() for _ in range(args.steps)]
+    torch.cuda.synchronize()
     start_evt.record(stream)
-    for _ in range(args.steps):
+    for lengths in step_lengths:
         for layer in range(L):
-            flash_attn_with_kvcache(q4, cache[0, layer], cache[1, layer], cache_seqlens=actx.context_lens,
+            flash_attn_with_kvcache(q4, cache[0, layer], cache[1, layer], cache_seqlens=lengths,
                                     block_table=actx.block_tables, softmax_scale=softmax_scale,
                                     causal=True)
     end_evt.record(stream)
@@ -495,7 +500,7 @@ def main(argv=None) -> int:
                     f"{r['gbps_at_p50']:.0f} GB/s")
 
     traffic = measured_traffic(PROFILE_FILE, "gather_planned_kernel", wl.gather_bytes(layers=1))
-    attn_traffic = measured_traffic(ATTENTION_PROFILE_FILE, "attn_decode_partial_kernel", attn_bytes)
+    attn_traffic = measured_traffic(ATTENTION_PROFILE_FILE, "attn_decode_", attn_bytes)
 
     cpu_baseline = None
     if not args.profile and args.cpu_baseline_layers > 0:
@@ -588,6 +593,7 @@ def main(argv=None) -> int:
         "attention": {
             "kernel": "paged_attention_decode (split-K partials + merge, one layer, 16 q heads "
                       "over 8 kv heads, straight from the paged cache)",
+            "partial_kernel": decode_kernel_name(8, 2),
             "us_bracketed": summarize_latencies(attn_us),
             "achieved": round(attn_bytes / (attn_mean * 1e-6) / 1e9, 2),
             "peak": MI355X_HBM_PEAK_GBPS,
@@ -686,9 +692,18 @@ def host_attention(q, k, v, scale: float, offset: int | None = None):
     return torch.matmul(torch.softmax(scores, dim=-1), values).transpose(0, 1)   # [Lq, Hq, D]
 
 
+def attention_tolerance(ref, ref_abs):
+    """Allowed error of a decode-attention output: 1e-3 + 2^-8 (|ref| +
+    ref_abs), ref_abs being the same attention over |V|.  The MFMA kernel
+    rounds its softmax weights to the input type (as flash attention does),
+    so an output near zero by cancellation carries the error of its terms;
+    the same bound holds the GPU tests."""
+    return 1e-3 + 2.0 ** -8 * (abs(ref) + ref_abs)
+
+
 def check_decode_attention(backend, case: dict, sample: int = 6) -> None:
     """The decode attention of ``sample`` sequences against host_attention
-    over their K/V rows gathered bit-exactly, within 1e-3 + 1e-2 |ref|."""
+    over their K/V rows gathered bit-exactly, within attention_tolerance."""
     import numpy as np
     import torch
 
@@ -697,11 +712,22 @@ def check_decode_attention(backend, case: dict, sample: int = 6) -> None:
     for i in np.linspace(0, len(case["lens"]) - 1, sample).astype(int).tolist():
         n = int(case["lens"][i])
         table = case["tables"][i, : -(-n // case["kc"].shape[1])].contiguous()
-        expect = host_attention(case["q"][i:i + 1], backend.gather(case["kc"], table, n),
-                                backend.gather(case["vc"], table, n), case["scale"])[0]
+        keys, values = backend.gather(case["kc"], table, n), backend.gather(case["vc"], table, n)
+        expect = host_attention(case["q"][i:i + 1], keys, values, case["scale"])[0]
+        expect_abs = host_attention(case["q"][i:i + 1], keys, values.abs(), case["scale"])[0]
         err = (case["out"][i].float().cpu() - expect).abs()
-        if bool((err > 1e-3 + 1e-2 * expect.abs()).any()):
+        if bool((err > attention_tolerance(expect, expect_abs)).any()):
             raise AssertionError(f"decode attention, sequence {i}: max error {float(err.max()):.3e}")
+
+
+def decode_kernel_name(kv_heads: int, group: int) -> str:
+    """The kernel nkv_paged_attention_decode runs for a head layout: the
+    MFMA kernel, or the VALU kernel for 1-2 query heads per kv head over 1,
+    2, 4 or 8 kv heads when NKV_DECODE_VALU=1 is set."""
+    import os
+
+    valu = os.environ.get("NKV_DECODE_VALU") == "1" and group <= 2 and kv_heads in (1, 2, 4, 8)
+    return "attn_decode_partial_kernel" if valu else "attn_decode_mfma_kernel"
 
 
 def measure_grouped_decode(device, backend, wl, reps: int) -> list[dict]:
@@ -730,7 +756,7 @@ def measure_grouped_decode(device, backend, wl, reps: int) -> list[dict]:
         achieved = case["bytes"] / (us * 1e-6) / 1e9
         records.append({
             "layout": name, "kv_heads": hkv, "q_heads_per_kv_head": g,
-            "kernel": "attn_decode_mfma_kernel" if g >= 3 else "attn_decode_partial_kernel",
+            "kernel": decode_kernel_name(hkv, g),
             "us": round(us, 2), "algorithmic_bytes": case["bytes"], "achieved": round(achieved, 1),
             "unit": "GB/s", "frac": round(achieved / MI355X_HBM_PEAK_GBPS, 4),
         })
@@ -1306,7 +1332,7 @@ def measure_reference_matrix(device, backend, iterations: int | None = None) -> 
 def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer,
                      workload_names) -> dict:
     """The CPU leg: the oracle checks the GPU's outputs of ``check_layers``
-    (store+gather bit-exact; attention within 1e-3 + 1e-2*|ref| of the fp32
+    (store+gather bit-exact; attention within attention_tolerance of the fp32
     oracle on 32 sequences); then the reference pytorch backend's torch ops
     are timed on host tensors (:func:`cpu_reference_baseline`, the figure
     the line reports), and the oracle's OpenMP C restatement beside them
@@ -1339,8 +1365,10 @@ def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer,
         sample = np.linspace(0, wl.num_seqs - 1, 32).astype(np.int64)
         ref = oracle.paged_attention_decode(got["q"][sample], hk, hv, ctables[sample],
                                             wl.num_tokens[sample], got["scale"])
+        ref_abs = oracle.paged_attention_decode(got["q"][sample], hk, hv & np.int16(0x7FFF),
+                                                ctables[sample], wl.num_tokens[sample], got["scale"])
         err = np.abs(got["attention"][sample] - ref)
-        if (err > 1e-3 + 1e-2 * np.abs(ref)).any():
+        if (err > attention_tolerance(ref, ref_abs)).any():
             raise AssertionError(f"decode step layer {layer}: attention differs from the oracle "
                                  f"(max err {err.max():.3e})")
         log(f"[bench] layer {layer}: store+gather bit-exact, attention max err {err.max():.2e} vs oracle")

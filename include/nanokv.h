@@ -332,10 +332,11 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  * with a result in the input type; scale must be finite and positive
  * (NKV_E_INVALID otherwise).  An empty context yields zeros.  dtype
  * NKV_DTYPE_BFLOAT16 or NKV_DTYPE_FLOAT16 (q, caches and out alike),
- * head_dim 128, any num_kv_heads, G <= 16.  G = 1 or 2 with 1, 2, 4 or 8
- * kv heads runs on the VALU kernel; every other layout runs on the MFMA
+ * head_dim 128, any num_kv_heads, G <= 16.  Every layout runs on the MFMA
  * kernel, which rounds the softmax weights to the input type before the
- * product with V, as flash attention does.
+ * product with V, as flash attention does.  With NKV_DECODE_VALU=1 in the
+ * environment (read on every call), G = 1 or 2 with 1, 2, 4 or 8 kv heads
+ * runs on the VALU kernel instead, which keeps the weights in fp32.
  *
  * Replaces: the decode call flash_attn_with_kvcache(q, k_cache, v_cache,
  *   cache_seqlens=context_lens, block_table=block_tables, softmax_scale,

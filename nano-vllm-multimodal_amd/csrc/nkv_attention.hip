@@ -13,8 +13,8 @@
 // max m, weight sum l, unnormalised output), and a reduce kernel merges the
 // partials of each (sequence, query head).  Two kernels write the partials:
 //
-// VALU kernel, G = Hq / Hkv = 1 or 2 (Hkv = 1, 2, 4, 8), one workgroup per
-// entry for all heads (8 waves):
+// VALU kernel, G = Hq / Hkv = 1 or 2 (Hkv = 1, 2, 4, 8), on request, one
+// workgroup per entry for all heads (8 waves):
 //   * the entry's cache rows are resolved once through the block table into
 //     LDS (invalid block ids give rows that are skipped);
 //   * a 16-lane DPP row owns one (row, kv head): each lane holds 8 dims
@@ -28,11 +28,15 @@
 //     its share of the query heads (fp16 sums with a power-of-two scale).
 // At G <= 2 its VALU work stays under the memory time.
 //
-// MFMA kernel, G = 3..16 and any other kv-head count: one workgroup per
-// (entry, kv head), the G query heads as the columns of 16x16 MFMA tiles
-// (see attn_decode_mfma_kernel); the VALU cost of 2 G FLOPs per cache byte
-// would outrun the memory time from G = 3 on.
+// MFMA kernel, G = 1..16 and any kv-head count (the default for every
+// layout): one workgroup per (entry, kv head), the G query heads as the
+// columns of 16x16 MFMA tiles (see attn_decode_mfma_kernel); the VALU cost
+// of 2 G FLOPs per cache byte would outrun the memory time from G = 3 on,
+// and with the kv head rotated over the XCDs the MFMA kernel is also the
+// faster one at G = 1 and 2.  The VALU kernel runs the G <= 2 layouts it
+// covers when NKV_DECODE_VALU=1 is set.
 #include <cmath>
+#include <cstdlib>
 
 #include "nkv_common.h"
 #include "nkv_mfma.h"
@@ -563,10 +567,20 @@ constexpr int kDecKeys = 16;                  // keys per chunk
 constexpr int kDecChunkWords = kDecKeys * 16;  // 16-byte words per K or V chunk
 constexpr int kDecCopies = 2 * kDecKeys / 4;   // copy instructions per chunk (K and V)
 constexpr int kDecMaxGroup = 16;               // query heads per kv head (MFMA columns)
+// Smallest G run on MFMA by default (smaller G: the VALU kernel).  With the
+// kv head rotated over the XCDs the MFMA kernel is the faster one on every
+// layout measured, G = 1 and 2 included (256-sequence decode step, one
+// layer, whole calls: 16 q / 8 kv 547.8 against 560.6-561.1 us, 8 / 8
+// 554.0-554.5 against 577.3-578.0, 8 / 4 289.9-290.0 against 302.5-303.6,
+// 4 / 2 152.5-152.6 against 156.6-157.1), so it serves every layout.  The
+// VALU kernel stays for the G <= 2 layouts it covers when NKV_DECODE_VALU=1
+// is set in the environment (read on every call).
 #ifndef NKV_DEC_MFMA_MIN_GROUP
-#define NKV_DEC_MFMA_MIN_GROUP 3  // smallest G run on MFMA (smaller G: the VALU kernel)
+#define NKV_DEC_MFMA_MIN_GROUP 1
 #endif
 constexpr int kDecMfmaMinGroup = NKV_DEC_MFMA_MIN_GROUP;
+// G below which the VALU kernel runs when NKV_DECODE_VALU=1 asks for it.
+constexpr int kDecValuMaxGroup = 2;
 static_assert(kDecWaves == 2 || kDecWaves == 4 || kDecWaves == 8,
               "NKV_DEC_WAVES must be 2, 4 or 8");
 static_assert(kDecSlots >= 2 && kDecSlots <= 4, "NKV_DEC_SLOTS must be in [2, 4]");
@@ -993,9 +1007,13 @@ extern "C" int nkv_paged_attention_decode(
                     "nkv_paged_attention_decode: num_q_heads must be a multiple of num_kv_heads");
   }
   const int64_t group = num_q_heads / num_kv_heads;
-  // MFMA from kDecMfmaMinGroup query heads per kv head on, and for every
-  // layout the VALU kernels do not cover; the VALU kernel below that.
-  bool use_mfma = group >= kDecMfmaMinGroup && group <= kDecMaxGroup;
+  // MFMA from kDecMfmaMinGroup query heads per kv head on (every layout by
+  // default), and for every layout the VALU kernels do not cover; the VALU
+  // kernel below that, or for G <= 2 when NKV_DECODE_VALU=1.
+  const char* valu_env = std::getenv("NKV_DECODE_VALU");
+  const bool valu_requested = valu_env != nullptr && valu_env[0] == '1' && valu_env[1] == '\0';
+  const int64_t mfma_min_group = valu_requested ? kDecValuMaxGroup + 1 : kDecMfmaMinGroup;
+  bool use_mfma = group >= mfma_min_group && group <= kDecMaxGroup;
   PartialKernel kernel = nullptr;
   if (!use_mfma) {
     kernel = half ? partial_kernel_for<true>(num_kv_heads, group)

@@ -14,6 +14,8 @@ different.
 from __future__ import annotations
 
 import math
+import threading
+import weakref
 
 import torch
 
@@ -69,12 +71,47 @@ def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu
                                             cu_seqlens_k, scale)
 
 
+class _StepPlan:
+    """The decode plan of the current step: every layer passes the same
+    cache_seqlens tensor, so the first call reads the context total back
+    once and builds the plan, and the other layers reuse both.  The entry is
+    tied to that tensor object (a weak reference), its version counter and
+    its shape, so a new step (a new tensor, or the same buffer rewritten: the
+    packer bumps the version of what it writes) builds a new plan."""
+
+    def __init__(self) -> None:
+        self._lock = threading.Lock()
+        self._entry = None  # (weakref to cache_seqlens, key, cu_seqlens_k, total, plan)
+
+    def lookup(self, cache_seqlens, key):
+        with self._lock:
+            entry = self._entry
+        if entry is not None and entry[0]() is cache_seqlens and entry[1] == key:
+            return entry[2:]
+        return None
+
+    def store(self, cache_seqlens, key, cu_seqlens_k, total, plan) -> None:
+        with self._lock:
+            self._entry = (weakref.ref(cache_seqlens), key, cu_seqlens_k, total, plan)
+
+
+_STEP_PLAN = _StepPlan()
+
+
 def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table=None,
                             softmax_scale=None, causal=False, **options):
     """One decode token per sequence over its paged context
     (attention.py:122-130): q [batch, 1, heads, 128], caches [blocks,
     block_size, kv_heads, 128], cache_seqlens [batch] int32 context lengths,
-    block_table [batch, width] int32.  Returns [batch, 1, heads, 128]."""
+    block_table [batch, width] int32.  Returns [batch, 1, heads, 128].
+
+    Outside graph capture the first call of a step reads the total context
+    length back (one synchronisation per step, not per layer) and builds a
+    plan of exactly the context's entries, which the step's other layers
+    reuse.  Under graph capture nothing may be read back: the plan is then
+    sized for the longest contexts the tables can hold (batch x width x
+    block_size rows), and its padding entries cost workgroups that exit at
+    once."""
     _check_options("flash_attn_with_kvcache", causal, options)
     if q.ndim != 4 or q.shape[1] != 1:
         raise NotImplementedError("flash_attn_with_kvcache: one query token per sequence only")
@@ -82,16 +119,24 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table
         raise NotImplementedError("flash_attn_with_kvcache: needs cache_seqlens and block_table")
     scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
     batch = q.shape[0]
-    lengths = cache_seqlens.to(device=q.device, dtype=torch.int32)
-    cu_seqlens_k = torch.zeros(batch + 1, dtype=torch.int32, device=q.device)
-    torch.cumsum(lengths, 0, out=cu_seqlens_k[1:])
-    # The plan is sized for the longest contexts the tables can hold, so the
-    # lengths are not read back to the host (unless the synchronising index
-    # checks are on, which compare the exact total).
-    if index_value_validation_enabled(lengths):
-        total = int(cu_seqlens_k[-1])
+    capturing = torch.cuda.is_current_stream_capturing()
+    key = (cache_seqlens.data_ptr(), cache_seqlens._version, tuple(cache_seqlens.shape),
+           str(q.device), int(k_cache.shape[1]))
+    cached = None if capturing else _STEP_PLAN.lookup(cache_seqlens, key)
+    if cached is not None:
+        cu_seqlens_k, total, plan = cached
     else:
-        total = batch * block_table.shape[1] * k_cache.shape[1]
+        lengths = cache_seqlens.to(device=q.device, dtype=torch.int32)
+        cu_seqlens_k = torch.zeros(batch + 1, dtype=torch.int32, device=q.device)
+        torch.cumsum(lengths, 0, out=cu_seqlens_k[1:])
+        if capturing and not index_value_validation_enabled(lengths):
+            total = batch * block_table.shape[1] * k_cache.shape[1]
+            plan = None
+        else:
+            total = int(cu_seqlens_k[-1])
+            plan = _BACKEND.build_attention_plan(k_cache, cu_seqlens_k, total)
+            if not capturing:
+                _STEP_PLAN.store(cache_seqlens, key, cu_seqlens_k, total, plan)
     out = _BACKEND.paged_attention_decode(q[:, 0], k_cache, v_cache, block_table, cu_seqlens_k,
-                                          total, scale)
+                                          total, scale, plan=plan)
     return out.unsqueeze(1)

@@ -22,6 +22,7 @@ from typing import Iterable, Sequence
 
 import numpy as np
 import torch
+from torch.autograd.graph import increment_version
 
 from nanokv import _lib
 from nanokv.paged_kv.ops import current_stream_handle
@@ -311,6 +312,12 @@ class DevicePacker:
             buffers.block_tables.data_ptr(), buffers.cu_seqlens_k.data_ptr(), self._stream(),
         )
         _lib.check(status, "nkv_pack_decode")
+        # The kernel wrote the buffers behind torch's back: bump their version
+        # counters, so whatever keys a cache on a tensor's version (the decode
+        # plan of nanokv.flash) sees the new contents.
+        for written in (buffers.slot_mapping, buffers.context_lens, buffers.block_tables,
+                        buffers.cu_seqlens_k):
+            increment_version(written)
         return Context(
             is_prefill=False,
             cu_seqlens_k=buffers.cu_seqlens_k[: b + 1],

@@ -2,11 +2,13 @@
 (oracle.paged_kv.paged_attention_decode, itself pinned to torch's SDPA with
 GQA in tests/test_attention_oracle.py).
 
-Two kernels serve the call: a VALU kernel for 1-2 query heads per kv head
-(kv heads 1, 2, 4 or 8) and an MFMA kernel for 3-16 query heads per kv head
-and every other kv-head count.  Scores and the softmax run in fp32 in both;
-the MFMA kernel rounds the weights p to bf16 / fp16 before the second
-product (as flash attention does), and both round the result once.  Each
+Two kernels serve the call: the MFMA kernel, the default for every layout
+(1-16 query heads per kv head, any kv-head count), and the VALU kernel,
+which runs 1-2 query heads per kv head over 1, 2, 4 or 8 kv heads when
+NKV_DECODE_VALU=1 is set; the tests marked "valu" set it.  Scores and the
+softmax run in fp32 in both; the MFMA kernel rounds the weights p to bf16 /
+fp16 before the second product (as flash attention does), and both round
+the result once.  Each
 rounding is <= 2^-9 relative, so an element differs from the fp32 result by
 at most 2^-9 * sum_k p_k |v_k| / sum_k p_k (the same attention over |V|,
 "ref_abs") plus 2^-9 * |ref|; the tests allow 1e-3 + 2^-8 * (ref_abs + |ref|)
@@ -24,6 +26,28 @@ import torch
 from oracle import paged_kv as oracle
 
 pytestmark = pytest.mark.gpu
+
+VALU_KV_HEADS = (1, 2, 4, 8)
+
+
+def with_kernels(layouts):
+    """(kernel, *layout) cases: "mfma" for every layout, "valu" as well for
+    the layouts the VALU kernel has (1-2 query heads over 1, 2, 4 or 8 kv
+    heads)."""
+    cases = []
+    for layout in layouts:
+        cases.append(("mfma", *layout))
+        if layout[1] <= 2 and layout[0] in VALU_KV_HEADS:
+            cases.append(("valu", *layout))
+    return cases
+
+
+def select_kernel(monkeypatch, kernel: str) -> None:
+    """The library reads NKV_DECODE_VALU on every call."""
+    if kernel == "valu":
+        monkeypatch.setenv("NKV_DECODE_VALU", "1")
+    else:
+        monkeypatch.delenv("NKV_DECODE_VALU", raising=False)
 
 ATOL = 1e-3
 
@@ -77,7 +101,7 @@ def build_case(device, hkv, g, bs, lens, seed, q_pad_heads=0, dtype=torch.bfloat
     return dev, host, int(cu[-1])
 
 
-@pytest.mark.parametrize("hkv,g,bs", [
+@pytest.mark.parametrize("kernel,hkv,g,bs", with_kernels([
     (8, 2, 256), (8, 2, 16), (2, 8, 256), (2, 8, 16), (4, 4, 16), (4, 2, 32),
     (8, 1, 16), (2, 1, 16), (1, 8, 16), (1, 1, 4), (2, 4, 8),
     (8, 2, 24), (2, 4, 1000),  # block sizes that are not powers of two (1000: entries of 500 rows)
@@ -85,8 +109,9 @@ def build_case(device, hkv, g, bs, lens, seed, q_pad_heads=0, dtype=torch.bfloat
     (8, 5, 16), (8, 8, 256),  # 40 and 64 query heads
     (2, 16, 16), (1, 12, 256), (4, 10, 24), (2, 9, 8),  # 9-16 query heads per kv head
     (3, 4, 16), (16, 2, 16), (6, 1, 32), (5, 3, 256),  # kv-head counts other than 1, 2, 4, 8
-])
-def test_decode_attention_matches_oracle(backend, gpu_device, hkv, g, bs):
+]))
+def test_decode_attention_matches_oracle(backend, gpu_device, monkeypatch, kernel, hkv, g, bs):
+    select_kernel(monkeypatch, kernel)
     lens = [0, 1, bs - 1, bs, bs + 1, 3 * bs + 7, 2, 5 * bs, 17, 1]
     dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=hkv * 100 + g * 10 + bs)
     scale = 1.0 / math.sqrt(128)
@@ -97,11 +122,13 @@ def test_decode_attention_matches_oracle(backend, gpu_device, hkv, g, bs):
     assert torch.all(out[0] == 0), "an empty context must give zeros"
 
 
-@pytest.mark.parametrize("hkv,g,bs", [(8, 2, 16), (2, 8, 256), (1, 1, 4), (4, 2, 24), (8, 6, 16),
-                                      (2, 16, 16), (3, 4, 24)])
-def test_decode_attention_float16_matches_oracle(backend, gpu_device, hkv, g, bs):
-    """float16 q and caches (v_dot2 on fp16 pairs, or the fp16 MFMAs), fp16
+@pytest.mark.parametrize("kernel,hkv,g,bs", with_kernels([
+    (8, 2, 16), (2, 8, 256), (1, 1, 4), (4, 2, 24), (8, 6, 16), (2, 16, 16), (3, 4, 24)]))
+def test_decode_attention_float16_matches_oracle(backend, gpu_device, monkeypatch, kernel, hkv, g,
+                                                 bs):
+    """float16 q and caches (the fp16 MFMAs, or v_dot2 on fp16 pairs), fp16
     output; the same tolerance holds (fp16 rounds to 2^-11)."""
+    select_kernel(monkeypatch, kernel)
     lens = [0, 1, bs - 1, bs, bs + 1, 3 * bs + 7, 2, 5 * bs, 17, 1]
     dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=hkv + g + bs,
                                   dtype=torch.float16)
@@ -112,11 +139,11 @@ def test_decode_attention_float16_matches_oracle(backend, gpu_device, hkv, g, bs
     check_close(out, ref, f"fp16 hkv={hkv} g={g} bs={bs}")
 
 
-@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
-def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device, hkv, g):
+@pytest.mark.parametrize("kernel,hkv,g", with_kernels([(8, 2), (2, 8)]))
+def test_strided_q_plan_reuse_and_out_buffer(backend, gpu_device, monkeypatch, kernel, hkv, g):
     """q with padding heads (row stride past Hq * 128), one plan reused by
-    two calls, and a caller-owned output buffer; VALU (8 x 2) and MFMA
-    (2 x 8) kernels."""
+    two calls, and a caller-owned output buffer."""
+    select_kernel(monkeypatch, kernel)
     lens = [300, 1, 513, 256, 40]
     dev, host, total = build_case(gpu_device, hkv, g, 256, lens, seed=7, q_pad_heads=16)
     assert dev["q"].stride(0) == (hkv * g + 16) * 128
@@ -153,13 +180,14 @@ def test_plan_for_other_lengths_is_rejected(backend, gpu_device):
                                        total, 0.1, plan=plan)
 
 
-@pytest.mark.parametrize("hkv,g,bs", [(8, 2, 16), (2, 4, 8), (4, 2, 4), (1, 1, 1024), (8, 4, 4),
-                                      (2, 8, 1024)])
-def test_long_contexts_over_small_blocks(backend, gpu_device, hkv, g, bs):
+@pytest.mark.parametrize("kernel,hkv,g,bs", with_kernels([
+    (8, 2, 16), (2, 4, 8), (4, 2, 4), (1, 1, 1024), (8, 4, 4), (2, 8, 1024)]))
+def test_long_contexts_over_small_blocks(backend, gpu_device, monkeypatch, kernel, hkv, g, bs):
     """Entries span many blocks (512 rows of 8- or 16-row blocks, 256 rows =
     64 blocks of 4 rows) or half of one (1024-row blocks); contexts of
     several entries with ragged tails; the plan's entries tile each context
     in order."""
+    select_kernel(monkeypatch, kernel)
     from nanokv import _lib
 
     rows = int(_lib.load_library().nkv_attention_entry_rows(bs))
@@ -225,11 +253,12 @@ def test_head_rotation_over_many_entries(backend, gpu_device, hkv, g):
     check_close(out, reference(host, scale), f"rotation hkv={hkv} g={g}")
 
 
-@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
-def test_invalid_block_ids_drop_their_rows(backend, gpu_device, hkv, g):
+@pytest.mark.parametrize("kernel,hkv,g", with_kernels([(8, 2), (2, 8)]))
+def test_invalid_block_ids_drop_their_rows(backend, gpu_device, monkeypatch, kernel, hkv, g):
     """A block id outside [0, num_blocks) (or -1) inside a context drops that
     block's rows, so the result equals attention over the remaining rows;
     the kernel never reads outside the cache."""
+    select_kernel(monkeypatch, kernel)
     bs = 16
     lens = [5 * bs, 3 * bs + 4, 2 * bs]
     dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=11)
@@ -253,14 +282,16 @@ def test_invalid_block_ids_drop_their_rows(backend, gpu_device, hkv, g):
     check_close(out, ref, "invalid blocks")
 
 
-@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 1), (1, 2), (2, 8), (4, 4)])
-def test_rows_outside_the_contexts_may_hold_any_bits(backend, gpu_device, hkv, g):
+@pytest.mark.parametrize("kernel,hkv,g", with_kernels([(8, 2), (2, 1), (1, 2), (2, 8), (4, 4)]))
+def test_rows_outside_the_contexts_may_hold_any_bits(backend, gpu_device, monkeypatch, kernel, hkv,
+                                                     g):
     """Cache rows no context owns may hold any bits (a cache from torch.empty,
     freed blocks): here NaN and +-Inf in block 0 (which no table uses), in
     the spare blocks and in the unwritten tail of every context's last
     block.  The kernels read such rows only as skipped rows, so the result
-    is the oracle's, finite, for the VALU kernel (G <= 2, including 2 and
-    4 rows per wavefront load) and the MFMA kernel."""
+    is the oracle's, finite, for the MFMA kernel and the VALU kernel (2 x 1
+    and 1 x 2 give it 2 and 4 rows per wavefront load)."""
+    select_kernel(monkeypatch, kernel)
     bs = 16
     lens = [1, 5, bs, 3 * bs + 7, 40, 2, 0]
     dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=hkv * 31 + g)
@@ -286,12 +317,13 @@ def test_rows_outside_the_contexts_may_hold_any_bits(backend, gpu_device, hkv, g
     check_close(out, reference(host, scale), f"any-bits rows hkv={hkv} g={g}")
 
 
-@pytest.mark.parametrize("hkv,g", [(8, 2), (8, 4)])
-def test_cache_over_4gib(backend, gpu_device, hkv, g):
+@pytest.mark.parametrize("kernel,hkv,g", with_kernels([(8, 2), (8, 4)]))
+def test_cache_over_4gib(backend, gpu_device, monkeypatch, kernel, hkv, g):
     """Caches larger than 4 GiB, whose row byte offsets need more than 32
     bits (the MFMA kernel's 64-bit-address instance; the VALU kernel always
     forms 64-bit offsets): the contexts' blocks are moved to the top of each
     cache."""
+    select_kernel(monkeypatch, kernel)
     bs = 256
     lens = [300, 700, 1, 513]
     dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=43)
@@ -314,11 +346,12 @@ def test_cache_over_4gib(backend, gpu_device, hkv, g):
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("hq", [16, 32])
-def test_decode_step_layer_full_size(backend, gpu_device, hq):
+@pytest.mark.parametrize("kernel,hq", [("mfma", 16), ("valu", 16), ("mfma", 32)])
+def test_decode_step_layer_full_size(backend, gpu_device, monkeypatch, kernel, hq):
     """One layer of the 256-sequence decode step (contexts log-uniform in
-    [256, 16384], 8 kv heads x 2 query heads each: the VALU kernel; with 4
-    query heads each: the MFMA kernel), every element checked."""
+    [256, 16384], 8 kv heads x 2 or 4 query heads each), every element
+    checked; 2 query heads per kv head on both kernels."""
+    select_kernel(monkeypatch, kernel)
     from nanokv import workloads
 
     wl = workloads.build("decode_step", num_layers=1)

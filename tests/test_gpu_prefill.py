@@ -378,6 +378,21 @@ def test_flash_varlen_contiguous_keys_matches_oracle(gpu_device):
     check_close(out, *reference(host, 0.1), "flash varlen contiguous")
 
 
+def check_decode(out, host, lengths, scale, what):
+    """Decode output [batch, 1, heads, 128] against the oracle within
+    1e-3 + 2^-8 (ref_abs + |ref|), ref_abs being the same attention over |V|
+    (the MFMA kernel rounds its weights to the input type, so an output near
+    zero by cancellation carries the error of its terms)."""
+    args = (host["q"], host["kc"])
+    tail = (host["tables"], np.array(lengths), scale)
+    ref = oracle.paged_attention_decode(*args, host["vc"], *tail, dtype=host["dtype"])
+    ref_abs = oracle.paged_attention_decode(*args, host["vc"] & np.int16(0x7FFF), *tail,
+                                            dtype=host["dtype"])
+    g = out[:, 0].float().cpu().numpy()
+    bad = np.abs(g - ref) > 1e-3 + 2.0 ** -8 * (ref_abs + np.abs(ref))
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements off, max err {np.abs(g - ref).max():.3e}"
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_flash_with_kvcache_matches_decode_oracle(gpu_device, dtype):
     """attention.py:122-130: flash_attn_with_kvcache(q.unsqueeze(1), k_cache,
@@ -391,10 +406,56 @@ def test_flash_with_kvcache_matches_decode_oracle(gpu_device, dtype):
     out = flash_attn_with_kvcache(dev["q"].unsqueeze(1), dev["kc"], dev["vc"], cache_seqlens=lens,
                                   block_table=dev["tables"], softmax_scale=0.088, causal=True)
     assert out.shape == (4, 1, 16, 128) and out.dtype == dtype
-    ref = oracle.paged_attention_decode(host["q"], host["kc"], host["vc"], host["tables"],
-                                        np.array(k_lens), 0.088, dtype=host["dtype"])
-    g = out[:, 0].float().cpu().numpy()
-    assert not (np.abs(g - ref) > 1e-3 + 1e-2 * np.abs(ref)).any()
+    check_decode(out, host, k_lens, 0.088, "flash_attn_with_kvcache")
+
+
+def test_flash_with_kvcache_plan_follows_each_step(gpu_device):
+    """The decode drop-in builds one plan per step (on its first call, after
+    one read of the context total) and reuses it while the same lengths
+    tensor comes back unchanged.  A changed tensor must rebuild it: an
+    in-place update (torch bumps its version), and a new batch packed into
+    the same graph buffers by the device packer (which bumps the versions of
+    what its kernel wrote).  The second batch's contexts are much longer than
+    the first's, so a stale plan would drop rows and miss the oracle."""
+    from nanokv import flash
+    from nanokv.packing import DecodeGraphBuffers, DevicePacker, SequenceBatch
+
+    bs = 16
+    long_lens = [1, 300, 17, 64]
+    dev, host = build_case(gpu_device, 8, 2, bs, [1] * 4, long_lens, seed=53)
+    q = dev["q"].unsqueeze(1)
+
+    def check(lengths_host, out, what):
+        check_decode(out, host, lengths_host, 0.088, what)
+
+    def call(lengths, tables):
+        return flash.flash_attn_with_kvcache(q, dev["kc"], dev["vc"], cache_seqlens=lengths,
+                                             block_table=tables, softmax_scale=0.088, causal=True)
+
+    lens = torch.tensor(long_lens, dtype=torch.int32, device=gpu_device)
+    check(long_lens, call(lens, dev["tables"]), "first call of a step")
+    plan = flash._STEP_PLAN.lookup(lens, (lens.data_ptr(), lens._version, tuple(lens.shape),
+                                          str(q.device), bs))
+    assert plan is not None, "the step's plan is kept for the next layer"
+    check(long_lens, call(lens, dev["tables"]), "second layer, same plan")
+    shorter = [1, 250, 10, 64]
+    lens.copy_(torch.tensor(shorter, dtype=torch.int32))
+    check(shorter, call(lens, dev["tables"]), "lengths updated in place")
+
+    width = host["tables"].shape[1]
+    buffers = DecodeGraphBuffers.allocate(gpu_device, max_num_seqs=4, max_blocks=width)
+    packer = DevicePacker(gpu_device, bs)
+
+    def pack(lengths_host):
+        lists = [host["tables"][i, :-(-n // bs)].tolist() for i, n in enumerate(lengths_host)]
+        packer.pack_decode_into(SequenceBatch.from_block_lists(lengths_host, lists), buffers)
+
+    short_lens = [1, 20, 5, 3]
+    pack(short_lens)
+    view = buffers.context_lens  # the same tensor object for both batches
+    check(short_lens, call(view, buffers.block_tables), "first packed batch")
+    pack(long_lens)
+    check(long_lens, call(view, buffers.block_tables), "second batch packed into the same buffers")
 
 
 def test_flash_dropins_reject_what_they_do_not_compute(gpu_device):
