@@ -72,27 +72,32 @@ def flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu
 
 
 class _StepPlan:
-    """The decode plan of the current step: every layer passes the same
-    cache_seqlens tensor, so the first call reads the context total back
-    once and builds the plan, and the other layers reuse both.  The entry is
-    tied to that tensor object (a weak reference), its version counter and
-    its shape, so a new step (a new tensor, or the same buffer rewritten: the
-    packer bumps the version of what it writes) builds a new plan."""
+    """The decode plan of the current step.  Every layer of a step passes the
+    same cache_seqlens tensor and its own cache, so the first call reads the
+    context total back once and builds the plan, and the step's other layers
+    reuse both.  The entry holds while the same tensor object comes back
+    (a weak reference) with the same shape, device and block size, and, where
+    torch tracks it, the same version (an in-place update, or the device
+    packer's writes, which bump it).  A layer's cache seen a second time
+    starts a new step and a new plan: this covers inference tensors
+    (torch.inference_mode), which carry no version counter."""
 
     def __init__(self) -> None:
         self._lock = threading.Lock()
-        self._entry = None  # (weakref to cache_seqlens, key, cu_seqlens_k, total, plan)
+        self._entry = None  # [weakref to cache_seqlens, key, cu_seqlens_k, total, plan, caches seen]
 
-    def lookup(self, cache_seqlens, key):
+    def lookup(self, cache_seqlens, key, cache_ptr: int):
         with self._lock:
             entry = self._entry
-        if entry is not None and entry[0]() is cache_seqlens and entry[1] == key:
-            return entry[2:]
-        return None
+            if (entry is None or entry[0]() is not cache_seqlens or entry[1] != key
+                    or cache_ptr in entry[5]):
+                return None
+            entry[5].add(cache_ptr)
+            return entry[2], entry[3], entry[4]
 
-    def store(self, cache_seqlens, key, cu_seqlens_k, total, plan) -> None:
+    def store(self, cache_seqlens, key, cache_ptr: int, cu_seqlens_k, total, plan) -> None:
         with self._lock:
-            self._entry = (weakref.ref(cache_seqlens), key, cu_seqlens_k, total, plan)
+            self._entry = [weakref.ref(cache_seqlens), key, cu_seqlens_k, total, plan, {cache_ptr}]
 
 
 _STEP_PLAN = _StepPlan()
@@ -108,7 +113,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table
     Outside graph capture the first call of a step reads the total context
     length back (one synchronisation per step, not per layer) and builds a
     plan of exactly the context's entries, which the step's other layers
-    reuse.  Under graph capture nothing may be read back: the plan is then
+    reuse (see _StepPlan for what ends a step).  Under graph capture nothing may be read back: the plan is then
     sized for the longest contexts the tables can hold (batch x width x
     block_size rows), and its padding entries cost workgroups that exit at
     once."""
@@ -120,9 +125,11 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table
     scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else float(softmax_scale)
     batch = q.shape[0]
     capturing = torch.cuda.is_current_stream_capturing()
-    key = (cache_seqlens.data_ptr(), cache_seqlens._version, tuple(cache_seqlens.shape),
-           str(q.device), int(k_cache.shape[1]))
-    cached = None if capturing else _STEP_PLAN.lookup(cache_seqlens, key)
+    version = None if cache_seqlens.is_inference() else cache_seqlens._version
+    key = (cache_seqlens.data_ptr(), version, tuple(cache_seqlens.shape), str(q.device),
+           int(k_cache.shape[1]))
+    cache_ptr = k_cache.data_ptr()
+    cached = None if capturing else _STEP_PLAN.lookup(cache_seqlens, key, cache_ptr)
     if cached is not None:
         cu_seqlens_k, total, plan = cached
     else:
@@ -136,7 +143,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table
             total = int(cu_seqlens_k[-1])
             plan = _BACKEND.build_attention_plan(k_cache, cu_seqlens_k, total)
             if not capturing:
-                _STEP_PLAN.store(cache_seqlens, key, cu_seqlens_k, total, plan)
+                _STEP_PLAN.store(cache_seqlens, key, cache_ptr, cu_seqlens_k, total, plan)
     out = _BACKEND.paged_attention_decode(q[:, 0], k_cache, v_cache, block_table, cu_seqlens_k,
                                           total, scale, plan=plan)
     return out.unsqueeze(1)

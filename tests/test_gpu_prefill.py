@@ -411,12 +411,13 @@ def test_flash_with_kvcache_matches_decode_oracle(gpu_device, dtype):
 
 def test_flash_with_kvcache_plan_follows_each_step(gpu_device):
     """The decode drop-in builds one plan per step (on its first call, after
-    one read of the context total) and reuses it while the same lengths
-    tensor comes back unchanged.  A changed tensor must rebuild it: an
-    in-place update (torch bumps its version), and a new batch packed into
-    the same graph buffers by the device packer (which bumps the versions of
-    what its kernel wrote).  The second batch's contexts are much longer than
-    the first's, so a stale plan would drop rows and miss the oracle."""
+    one read of the context total) and reuses it for the step's other
+    layers, which pass the same lengths tensor and caches of their own.  It
+    must rebuild when the lengths change: an in-place update (torch bumps
+    the tensor's version), a new batch packed into the same graph buffers by
+    the device packer (which bumps the versions of what its kernel wrote),
+    and a layer's cache coming back (the next step).  The longer contexts
+    come second, so a stale plan would drop rows and miss the oracle."""
     from nanokv import flash
     from nanokv.packing import DecodeGraphBuffers, DevicePacker, SequenceBatch
 
@@ -424,23 +425,29 @@ def test_flash_with_kvcache_plan_follows_each_step(gpu_device):
     long_lens = [1, 300, 17, 64]
     dev, host = build_case(gpu_device, 8, 2, bs, [1] * 4, long_lens, seed=53)
     q = dev["q"].unsqueeze(1)
+    # three "layers": the same cache contents at three addresses
+    layers = [(dev["kc"], dev["vc"])] + [(dev["kc"].clone(), dev["vc"].clone()) for _ in range(2)]
 
-    def check(lengths_host, out, what):
+    def run(lengths, tables, layer, lengths_host, what):
+        kc, vc = layers[layer]
+        out = flash.flash_attn_with_kvcache(q, kc, vc, cache_seqlens=lengths, block_table=tables,
+                                            softmax_scale=0.088, causal=True)
         check_decode(out, host, lengths_host, 0.088, what)
 
-    def call(lengths, tables):
-        return flash.flash_attn_with_kvcache(q, dev["kc"], dev["vc"], cache_seqlens=lengths,
-                                             block_table=tables, softmax_scale=0.088, causal=True)
-
-    lens = torch.tensor(long_lens, dtype=torch.int32, device=gpu_device)
-    check(long_lens, call(lens, dev["tables"]), "first call of a step")
-    plan = flash._STEP_PLAN.lookup(lens, (lens.data_ptr(), lens._version, tuple(lens.shape),
-                                          str(q.device), bs))
-    assert plan is not None, "the step's plan is kept for the next layer"
-    check(long_lens, call(lens, dev["tables"]), "second layer, same plan")
-    shorter = [1, 250, 10, 64]
-    lens.copy_(torch.tensor(shorter, dtype=torch.int32))
-    check(shorter, call(lens, dev["tables"]), "lengths updated in place")
+    short_lens = [1, 20, 5, 3]
+    lens = torch.tensor(short_lens, dtype=torch.int32, device=gpu_device)
+    run(lens, dev["tables"], 0, short_lens, "first layer of a step")
+    entry = flash._STEP_PLAN._entry
+    run(lens, dev["tables"], 1, short_lens, "second layer")
+    assert flash._STEP_PLAN._entry is entry, "the step's plan is reused by its next layer"
+    lens.copy_(torch.tensor(long_lens, dtype=torch.int32))
+    run(lens, dev["tables"], 2, long_lens, "lengths updated in place (version)")
+    assert flash._STEP_PLAN._entry is not entry
+    entry = flash._STEP_PLAN._entry
+    run(lens, dev["tables"], 0, long_lens, "a layer not yet seen with this plan")
+    assert flash._STEP_PLAN._entry is entry
+    run(lens, dev["tables"], 2, long_lens, "a layer's cache again: the next step")
+    assert flash._STEP_PLAN._entry is not entry
 
     width = host["tables"].shape[1]
     buffers = DecodeGraphBuffers.allocate(gpu_device, max_num_seqs=4, max_blocks=width)
@@ -450,12 +457,21 @@ def test_flash_with_kvcache_plan_follows_each_step(gpu_device):
         lists = [host["tables"][i, :-(-n // bs)].tolist() for i, n in enumerate(lengths_host)]
         packer.pack_decode_into(SequenceBatch.from_block_lists(lengths_host, lists), buffers)
 
-    short_lens = [1, 20, 5, 3]
     pack(short_lens)
     view = buffers.context_lens  # the same tensor object for both batches
-    check(short_lens, call(view, buffers.block_tables), "first packed batch")
+    run(view, buffers.block_tables, 1, short_lens, "first packed batch")
     pack(long_lens)
-    check(long_lens, call(view, buffers.block_tables), "second batch packed into the same buffers")
+    run(view, buffers.block_tables, 2, long_lens, "second batch packed into the same buffers")
+
+    # the reference's engine runs under torch.inference_mode(): its lengths
+    # carry no version counter, and a step is told by the layers' caches
+    with torch.inference_mode():
+        lens_inf = torch.tensor(long_lens, dtype=torch.int32, device=gpu_device)
+        assert lens_inf.is_inference()
+        run(lens_inf, dev["tables"], 0, long_lens, "inference tensor, first layer")
+        entry = flash._STEP_PLAN._entry
+        run(lens_inf, dev["tables"], 1, long_lens, "inference tensor, second layer")
+        assert flash._STEP_PLAN._entry is entry
 
 
 def test_flash_dropins_reject_what_they_do_not_compute(gpu_device):
