@@ -843,63 +843,65 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_mfma_kernel(
   }
 }
 
-// Merges the partials of one (sequence, query head): the 4 waves of the
-// workgroup take the max of the parts' references together, then each walks
-// a quarter of the parts (two dims per lane from one fp16 pair, unrolled so
-// several loads are in flight), and wave 0 adds the four sums and divides
-// once.
-constexpr int kReduceWaves = 4;
+// Merges the partials of (sequence, query head) pairs, one wavefront per
+// pair and no LDS or barrier: lane i loads part i's (m + k, l 2^-k), and
+// every lane loads its two dims (one fp16 pair) of up to kReduceBatch parts
+// in the same round trip, so the merge waits for memory twice (the
+// sequence's part range, then the parts) instead of three times.  The wave
+// takes the parts' max with lane shuffles, weights and sums the parts in
+// fp32 (part i's m and l come from lane i by shuffle) and divides once.  A
+// context of more than kReduceBatch parts goes in batches, the running sums
+// rescaled when a later batch raises the max.
+constexpr int kReduceWaves = 4;  // pairs per workgroup
 constexpr int kReduceThreads = kReduceWaves * kWave;
+constexpr int kReduceBatch = 8;  // parts in flight per lane (contexts up to 6144 rows at 768 per part)
 
 template <bool kHalf>
 __global__ __launch_bounds__(kReduceThreads) void attn_decode_reduce_kernel(
     const uint32_t* __restrict__ part_acc, const f32x2* __restrict__ part_ml,
-    const int32_t* __restrict__ first_part, int64_t capacity, int32_t num_q_heads,
-    uint16_t* __restrict__ out, int64_t out_seq_stride) {
-  __shared__ float s_max[kReduceWaves];
-  __shared__ float s_acc[kReduceWaves][kHeadDim];
-  __shared__ float s_l[kReduceWaves];
-  const int32_t seq = blockIdx.x;
-  const int32_t qh = blockIdx.y;
+    const int32_t* __restrict__ first_part, int64_t capacity, int32_t num_seqs,
+    int32_t num_q_heads, uint16_t* __restrict__ out, int64_t out_seq_stride) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int64_t pair = static_cast<int64_t>(blockIdx.x) * kReduceWaves + wave;
+  if (pair >= static_cast<int64_t>(num_seqs) * num_q_heads) return;  // whole waves; no barrier
+  const int32_t seq = static_cast<int32_t>(pair / num_q_heads);
+  const int32_t qh = static_cast<int32_t>(pair % num_q_heads);
   const int64_t p0 = max(0, first_part[seq]);
   const int64_t p1 = min(capacity, static_cast<int64_t>(first_part[seq + 1]));
 
-  float mm = -INFINITY;
-  for (int64_t p = p0 + threadIdx.x; p < p1; p += kReduceThreads) {
-    mm = fmaxf(mm, part_ml[p * num_q_heads + qh].x);
-  }
-#pragma unroll
-  for (int d = kWave / 2; d > 0; d >>= 1) mm = fmaxf(mm, __shfl_xor(mm, d, kWave));
-  if (lane == 0) s_max[wave] = mm;
-  __syncthreads();
-#pragma unroll
-  for (int w = 0; w < kReduceWaves; ++w) mm = fmaxf(mm, s_max[w]);
-
+  float run_max = -INFINITY;  // max of the parts merged so far
   float ax = 0.f, ay = 0.f, lsum = 0.f;
-  if (mm != -INFINITY) {
-#pragma unroll 8
-    for (int64_t p = p0 + wave; p < p1; p += kReduceWaves) {
-      const f32x2 ml = part_ml[p * num_q_heads + qh];  // (m + k, l * 2^-k)
-      const uint32_t v = part_acc[(p * num_q_heads + qh) * (kHeadDim / 2) + lane];
-      const float f = exp2_fast(ml.x - mm);
-      ax = fmaf(half_lo(v), f, ax);
-      ay = fmaf(half_hi(v), f, ay);
-      lsum = fmaf(ml.y, f, lsum);
-    }
-  }
-  s_acc[wave][2 * lane] = ax;
-  s_acc[wave][2 * lane + 1] = ay;
-  if (lane == 0) s_l[wave] = lsum;
-  __syncthreads();
-  if (wave != 0) return;  // no barrier follows
-  ax = ay = lsum = 0.f;
+  for (int64_t b = p0; b < p1; b += kReduceBatch) {
+    const int n = static_cast<int>(min(static_cast<int64_t>(kReduceBatch), p1 - b));
+    f32x2 ml = {-INFINITY, 0.f};  // lane i < n: part b + i's (m + k, l 2^-k)
+    if (lane < n) ml = part_ml[(b + lane) * num_q_heads + qh];
+    uint32_t v[kReduceBatch];
 #pragma unroll
-  for (int w = 0; w < kReduceWaves; ++w) {
-    ax += s_acc[w][2 * lane];
-    ay += s_acc[w][2 * lane + 1];
-    lsum += s_l[w];
+    for (int i = 0; i < kReduceBatch; ++i) {
+      v[i] = i < n ? part_acc[((b + i) * num_q_heads + qh) * (kHeadDim / 2) + lane] : 0u;
+    }
+    float m = ml.x;
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, kWave));
+    const float new_max = fmaxf(run_max, m);
+    if (new_max == -INFINITY) continue;  // nothing valid yet (uniform across the wave)
+    const float keep = exp2_fast(run_max - new_max);  // 0 while run_max is -inf
+    ax *= keep;
+    ay *= keep;
+    lsum *= keep;
+#pragma unroll
+    for (int i = 0; i < kReduceBatch; ++i) {
+      if (i < n) {
+        const float mi = __shfl(ml.x, i, kWave);
+        const float li = __shfl(ml.y, i, kWave);
+        const float f = mi == -INFINITY ? 0.f : exp2_fast(mi - new_max);
+        ax = fmaf(half_lo(v[i]), f, ax);
+        ay = fmaf(half_hi(v[i]), f, ay);
+        lsum = fmaf(li, f, lsum);
+      }
+    }
+    run_max = new_max;
   }
   const bool any = lsum > 0.f;
   const uint32_t packed = static_cast<uint32_t>(from_f32<kHalf>(any ? ax / lsum : 0.f)) |
@@ -1088,15 +1090,17 @@ extern "C" int nkv_paged_attention_decode(
         part_ml);
     if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
   }
-  const dim3 reduce_grid(static_cast<unsigned>(num_seqs), static_cast<unsigned>(num_q_heads));
+  // one wavefront per (sequence, query head) pair, kReduceWaves pairs per workgroup
+  const int64_t pairs = num_seqs * num_q_heads;
+  const dim3 reduce_grid(static_cast<unsigned>((pairs + kReduceWaves - 1) / kReduceWaves));
   if (half) {
     attn_decode_reduce_kernel<true><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
-        static_cast<uint16_t*>(out), out_seq_stride);
+        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_seqs),
+        static_cast<int32_t>(num_q_heads), static_cast<uint16_t*>(out), out_seq_stride);
   } else {
     attn_decode_reduce_kernel<false><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_q_heads),
-        static_cast<uint16_t*>(out), out_seq_stride);
+        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_seqs),
+        static_cast<int32_t>(num_q_heads), static_cast<uint16_t*>(out), out_seq_stride);
   }
   return nkv_check_launch("nkv_paged_attention_decode (reduce)");
 }
