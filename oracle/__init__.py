@@ -3,7 +3,7 @@ and of its model-runner metadata packing.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg may import or run anything under oracle/, and
-only as the checker (or the timed CPU baseline), never as the thing measured
+only to check results (or as the timed CPU baseline), never as the thing measured
 or shipped.  The product (nano-vllm-multimodal_amd/) never imports it and
 fails loudly when its HIP library is missing.
 

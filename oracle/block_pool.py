@@ -3,7 +3,7 @@ free-block FIFO, the reference counts and the per-sequence block tables
 (nanovllm/engine/block_manager.py:87-118, 159-227).
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product imports this module: only
-tests/ use it, as the checker of the device block pool.
+tests/ use it, to check the device block pool against it.
 
 The prefix-hash chain (compute_hash, hash_to_block_id, cache_key
 verification, hash_blocks; block_manager.py:65-85, 229-258) stays with the

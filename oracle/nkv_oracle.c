@@ -2,7 +2,7 @@
  * CPU restatement of the reference's paged-KV hot path in plain C.
  *
  * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg (as the checker and the timed CPU baseline),
+ * bench.py's cpu_baseline leg (to check results, and as the timed CPU baseline),
  * never by the product.  Rows are opaque byte strings (row_bytes =
  * kv_heads*head_dim*element size), so results are bit-exact by construction.
  * Loops over tokens / blocks / sequences run under OpenMP with `threads`

@@ -2,8 +2,8 @@
 Python).
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product imports this module: only
-tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as
-the checker.  It works on raw element words (any numpy dtype of the right
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, to
+check results.  It works on raw element words (any numpy dtype of the right
 width; bf16 tensors are passed as int16 views), so every comparison against
 it is bit-exact.
 

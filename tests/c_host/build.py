@@ -3,7 +3,7 @@
 
 gcc compiles the C program against include/nanokv.h and the HIP runtime's C
 API, and links libnanokv.so (the product) and the oracle's C restatement
-(oracle/_build/libnkv_oracle.so, the checker) through run paths relative to
+(oracle/_build/libnkv_oracle.so, which checks the results) through run paths relative to
 the binary, so the built tree runs wherever it is copied.  Both libraries
 must be built first (``__graft_entry__.build()`` builds all three in order).
 """
