@@ -13,7 +13,9 @@ bf16), 256 live sequences with contexts log-uniform in [256, 16384] after
 Prints one JSON line:  value = store+gather algorithmic GB/s of the step
 (sum of the bytes the store and gather must move / step time), plus
 decode tokens/s, the HBM roofline of the dominant kernel (the varlen
-gather, timed live with events on its stream) and a CPU baseline: the
+gather, timed live with events on its stream, and checked against a
+rocprofv3 kernel trace of the same step taken on the same host before the
+timed run, "rocprof_same_host") and a CPU baseline: the
 reference pytorch backend's torch ops (index_copy_ store, index_select
 gather) on host tensors with every host thread, over the same step and the
 single-layer configurations, with the oracle's OpenMP C restatement timed
@@ -130,12 +132,40 @@ def parse_args(argv=None):
                         "cases), print one line, exit")
     p.add_argument("--cpu-baseline-workloads", default="decode_store,chunked_prefill,prefix_gather,narrow_rows",
                    help="single-layer configurations the CPU baseline also times ('' = none)")
+    p.add_argument("--settle-s", type=float, default=8.0,
+                   help="seconds the GPU idles after the decode-step cache is filled, before "
+                        "anything is timed (0 = none)")
+    p.add_argument("--no-rocprof-check", dest="rocprof_check", action="store_false",
+                   help="skip the same-host rocprofv3 kernel trace of the decode step that the "
+                        "roofline is checked against")
     args = p.parse_args(argv)
     if bool(args.case) != bool(args.profile_replay):
         p.error("--case and --profile-replay go together")
     if args.profile_replay < 0:
         p.error("--profile-replay must be positive")
     return args
+
+
+def same_host_roofline(trace: dict | None, launch_bytes: int, launch_us: float) -> dict | None:
+    """The gather's figures from the kernel trace taken on this host
+    (``nanokv.profiling.trace_kernel_here``): mean and median duration over
+    the replay's 280 launches, the fraction of peak at the mean, and the
+    ratio of the event-timed back-to-back duration to the trace's mean."""
+    if trace is None:
+        return None
+    if "error" in trace:
+        return {"error": trace["error"]}
+    from nanokv.benchmark import MI355X_HBM_PEAK_GBPS
+
+    return {
+        "kernel": trace["kernel"],
+        "dispatches": trace["dispatches"],
+        "mean_us": round(trace["mean_us"], 2),
+        "median_us": round(trace["median_us"], 2),
+        "frac_at_mean": round(launch_bytes / (trace["mean_us"] * 1e3) / MI355X_HBM_PEAK_GBPS, 4),
+        "events_over_trace_mean": round(launch_us / trace["mean_us"], 4),
+        "command": trace["command"],
+    }
 
 
 def reference_backend():
@@ -158,6 +188,19 @@ def main(argv=None) -> int:
               "runs it on its own kv heads with the same slot_mapping and block tables)",
               file=sys.stderr)
         return 2
+
+    # The decode step's kernel trace on this host, for the roofline's
+    # cross-check: a rocprofv3 child process that replays the step, run
+    # before this process touches the GPU (so the child has the whole HBM).
+    same_host_trace = None
+    if (args.rocprof_check and not args.case and not args.profile and not args.prefill_only
+            and not args.copy_calibration_mib and args.layers == 28):
+        from nanokv.profiling import trace_kernel_here
+
+        log("[bench] rocprofv3 kernel trace of the decode step on this host")
+        same_host_trace = trace_kernel_here("decode_step", "gather_planned_kernel", replay=10,
+                                            settle_s=args.settle_s)
+        log(f"[bench] same-host trace: {same_host_trace.get('median_us', same_host_trace.get('error'))}")
 
     import numpy as np
     import torch
@@ -229,6 +272,14 @@ def main(argv=None) -> int:
     for kv in range(2):
         for layer in range(L):
             cache[kv, layer].normal_(generator=g)
+    if args.settle_s > 0:
+        # The GPU idles before anything is timed: for a few seconds after a
+        # process frees a large allocation (the GPU tests, the trace child
+        # above), other GPU activity takes about 3% of HBM bandwidth
+        # (gathers 1,192-1,203 against 1,154-1,170 us for ~3.5 s after a
+        # process freed 120 GB; no slow phase after a 10 s wait).
+        torch.cuda.synchronize(device)
+        time.sleep(args.settle_s)
     new_k = wl.key.to(device)
     new_v = wl.value.to(device)
     offsets, ids = wl.csr()
@@ -562,6 +613,7 @@ def main(argv=None) -> int:
         },
         "hbm_fraction": round(gbps / MI355X_HBM_PEAK_GBPS, 4),
         "decode_tokens_per_s": round(B / (step_ms * 1e-3), 2),
+        "settle_s": args.settle_s,
         "step_bytes": step_bytes,
         "reference_effective_bytes_per_step": L * (
             effective_bytes("store", B, wl.num_kv_heads, wl.head_dim, 2)
@@ -589,6 +641,8 @@ def main(argv=None) -> int:
             "within_step": consistent,
             "rocprof_median_us": profiled,
             "rocprof_source": str(PROFILE_FILE.relative_to(REPO_ROOT)) if profiled else None,
+            "rocprof_same_host": same_host_roofline(same_host_trace, gather_launch_bytes,
+                                                    gather_launch_us),
         },
         "attention": {
             "kernel": "paged_attention_decode (split-K partials + merge, one layer, 16 q heads "

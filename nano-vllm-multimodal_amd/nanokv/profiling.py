@@ -57,11 +57,13 @@ COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 def trace_command(case: str, out_dir: str | Path, *, replay: int = 20, stem: str = "trace",
                   python: str = "python3", bench: str = "bench.py",
-                  rocprof: str = "rocprofv3") -> list[str]:
-    """Kernel trace + per-kernel stats of ``replay`` replays of one case."""
+                  rocprof: str = "rocprofv3", settle_s: float | None = None) -> list[str]:
+    """Kernel trace + per-kernel stats of ``replay`` replays of one case
+    (``settle_s``: the decode-step cases' idle seconds before the replays)."""
     _check_case(case, replay)
+    settle = [] if settle_s is None else ["--settle-s", f"{settle_s:g}"]
     return [rocprof, "--kernel-trace", "--stats", "--output-format", "csv", "-d", str(out_dir),
-            "-o", stem, "--", python, bench, "--case", case, "--profile-replay", str(replay)]
+            "-o", stem, "--", python, bench, "--case", case, "--profile-replay", str(replay), *settle]
 
 
 def counter_command(case: str | None, counter: str, out_dir: str | Path, *, replay: int = 3,
@@ -100,6 +102,57 @@ def collection_plan(case: str, out: Path, *, replay: int = 20, counter_replay: i
         ("copy_fetch", counter_command(None, "FETCH_SIZE", out / "copy_fetch", python=python)),
         ("copy_write", counter_command(None, "WRITE_SIZE", out / "copy_write", python=python)),
     ]
+
+
+def trace_kernel_here(case: str, kernel_prefix: str, *, replay: int = 10, timeout_s: int = 300,
+                      bench: str | Path | None = None, settle_s: float | None = None) -> dict:
+    """Run ``trace_command(case)`` as a child process on this host (in a
+    scratch directory under /tmp, TMPDIR=/tmp, the program straight after
+    ``--``) and return the trace statistics of the first kernel whose short
+    name starts with ``kernel_prefix`` (warmup dispatch skipped), with the
+    command.  Never raises: a missing profiler, a time-out or output without
+    that kernel gives ``{"error": ...}``.  rocprofv3 may exit non-zero after
+    the program finished and wrote its trace; the trace is used whenever the
+    replay printed its last line."""
+    import shutil
+    import signal
+    import tempfile
+
+    rocprof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3"
+                                             if os.path.exists("/opt/rocm/bin/rocprofv3") else None)
+    if rocprof is None:
+        return {"error": "rocprofv3 not found"}
+    bench_path = str(Path(bench) if bench else Path(__file__).resolve().parents[2] / "bench.py")
+    scratch = tempfile.mkdtemp(prefix="nanokv_trace_", dir="/tmp")
+    try:
+        command = trace_command(case, Path(scratch) / "trace", replay=replay, python=sys.executable,
+                                bench=bench_path, rocprof=rocprof, settle_s=settle_s)
+        env = dict(os.environ, TMPDIR="/tmp")
+        proc = subprocess.Popen(command, cwd="/tmp", env=env, stdout=subprocess.PIPE,
+                                stderr=subprocess.STDOUT, text=True, start_new_session=True)
+        try:
+            output, _ = proc.communicate(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.communicate()
+            return {"error": f"trace of {case} did not finish in {timeout_s} s"}
+        if "profile replay complete" not in output:
+            tail = output.strip().splitlines()[-3:]
+            return {"error": f"replay of {case} did not complete (exit {proc.returncode}): "
+                             + " | ".join(tail)}
+        try:
+            trace = kernel_durations(read_kernel_trace(_find_csv(Path(scratch) / "trace",
+                                                                 "_kernel_trace.csv")),
+                                     skip_first=1)
+        except (OSError, ValueError, KeyError) as exc:
+            return {"error": f"no kernel trace: {exc}"}
+        name = next((k for k in trace if k.startswith(kernel_prefix)), None)
+        if name is None:
+            return {"error": f"no {kernel_prefix}* dispatch in the trace"}
+        return {"kernel": name, **trace[name], "rocprof_exit": proc.returncode,
+                "command": " ".join([os.path.basename(rocprof), *command[1:]])}
+    finally:
+        shutil.rmtree(scratch, ignore_errors=True)
 
 
 # ------------------------------------------------------------------- parsing

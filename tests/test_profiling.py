@@ -171,3 +171,78 @@ def test_prefill_flops_match_the_bench_workload():
     total = int(workloads.build("decode_step", num_layers=1).num_tokens.sum())
     assert profiling.algorithmic_bytes_for("grouped_decode_2x8") == {
         "attn_decode_mfma_kernel": total * 2 * 128 * 2 * 2 + 2 * 256 * 16 * 128 * 2}
+
+
+FAKE_ROCPROF = '''#!{python}
+"""Stand-in for rocprofv3 in these CPU tests: writes a kernel trace of
+{n} gather dispatches into the -d directory, prints the replay's last line
+(or sleeps, or prints nothing, as the test asks)."""
+import csv, os, sys, time
+args = sys.argv[1:]
+mode = os.environ.get("FAKE_ROCPROF_MODE", "ok")
+if mode == "hang":
+    time.sleep(60)
+out = os.path.join(args[args.index("-d") + 1], "host")
+os.makedirs(out, exist_ok=True)
+columns = {columns!r}
+with open(os.path.join(out, args[args.index("-o") + 1] + "_kernel_trace.csv"), "w", newline="") as f:
+    w = csv.DictWriter(f, columns)
+    w.writeheader()
+    for i in range({n}):
+        row = dict.fromkeys(columns, 0)
+        row.update(Dispatch_Id=i + 1, Kernel_Name={gather!r}, Start_Timestamp=1000 * i,
+                   End_Timestamp=1000 * i + (5000 if i == 0 else 1100 + i % 3 * 10))
+        w.writerow(row)
+if mode == "ok":
+    print("profile replay complete: " + args[args.index("--case") + 1])
+sys.exit(139 if mode == "ok" else 1)
+'''
+
+
+def fake_rocprof(tmp_path, monkeypatch, mode="ok", n=7):
+    import sys
+
+    bin_dir = tmp_path / "bin"
+    bin_dir.mkdir()
+    script = bin_dir / "rocprofv3"
+    script.write_text(FAKE_ROCPROF.format(python=sys.executable, n=n, columns=TRACE_COLUMNS,
+                                          gather=GATHER))
+    script.chmod(0o755)
+    monkeypatch.setenv("PATH", f"{bin_dir}:{__import__('os').environ['PATH']}")
+    monkeypatch.setenv("FAKE_ROCPROF_MODE", mode)
+
+
+def test_trace_on_this_host_reads_the_replays_kernel(tmp_path, monkeypatch):
+    """trace_kernel_here runs the case's trace command as a child, skips the
+    first dispatch, and keeps the trace even when the profiler exits
+    non-zero after the replay's last line (as rocprofv3 can)."""
+    fake_rocprof(tmp_path, monkeypatch, n=7)
+    got = profiling.trace_kernel_here("decode_step", "gather_planned_kernel", replay=10, timeout_s=60)
+    assert got["kernel"] == "gather_planned_kernel<16, false>"
+    assert got["dispatches"] == 6  # the 5 us first dispatch skipped
+    assert got["median_us"] == pytest.approx(1.11)
+    assert got["mean_us"] == pytest.approx((1.11 + 1.12 + 1.10 + 1.11 + 1.12 + 1.10) / 6)
+    assert got["rocprof_exit"] == 139
+    command = got["command"].split()
+    assert command[0] == "rocprofv3" and command[command.index("--") + 2].endswith("bench.py")
+    assert command[-4:] == ["--case", "decode_step", "--profile-replay", "10"]
+
+
+@pytest.mark.parametrize("mode,timeout,what", [("hang", 2, "did not finish"),
+                                                ("silent", 60, "did not complete")])
+def test_trace_on_this_host_reports_failures(tmp_path, monkeypatch, mode, timeout, what):
+    fake_rocprof(tmp_path, monkeypatch, mode=mode)
+    got = profiling.trace_kernel_here("decode_step", "gather_planned_kernel", timeout_s=timeout)
+    assert what in got["error"]
+
+
+def test_same_host_roofline_record():
+    import bench
+
+    trace = {"kernel": "gather_planned_kernel<16, false>", "dispatches": 270, "mean_us": 1150.0,
+             "median_us": 1140.0, "command": "rocprofv3 ..."}
+    got = bench.same_host_roofline(trace, 7_300_773_108, 1160.0)
+    assert got["frac_at_mean"] == pytest.approx(7_300_773_108 / 1150e3 / 8000, abs=1e-4)
+    assert got["events_over_trace_mean"] == pytest.approx(1160 / 1150, abs=1e-4)
+    assert bench.same_host_roofline({"error": "x"}, 1, 1.0) == {"error": "x"}
+    assert bench.same_host_roofline(None, 1, 1.0) is None
