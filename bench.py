@@ -536,11 +536,15 @@ def main(argv=None) -> int:
                     "on the same GPU",
             "decode_step": measure_torch_reference_step(wl, device, cache, new_k, new_v, batch,
                                                         packer, step_ms),
+            "decode_step_hip_backend_unchanged_sdpa": measure_torch_reference_step(
+                wl, device, cache, new_k, new_v, batch, packer, step_ms, ref=backend),
             "microbenchmark": measure_reference_matrix(device, backend),
         }
         log(f"[bench] torch reference decode step: "
             f"{gpu_reference['decode_step']['ms_per_step']:.1f} ms/step "
-            f"({gpu_reference['decode_step']['speedup_of_hip']:.1f}x slower than hip)")
+            f"({gpu_reference['decode_step']['speedup_of_hip']:.1f}x slower than hip); the hip "
+            f"backend driven the same way: "
+            f"{gpu_reference['decode_step_hip_backend_unchanged_sdpa']['ms_per_step']:.1f} ms/step")
 
     other_workloads = None
     if args.workload_iterations > 0 and not args.profile:
@@ -1258,16 +1262,19 @@ def measure_block_pool(wl, device, packer, batch, steps: int, warmup: int) -> di
 
 
 def measure_torch_reference_step(wl, device, cache, new_k, new_v, batch, packer,
-                                 hip_step_ms: float, steps: int = 2) -> dict:
+                                 hip_step_ms: float, steps: int = 2, ref=None) -> dict:
     """The decode step's data path as the reference's SDPA decode drives its
     backend (nanovllm/layers/attention.py:75-93, 284-300): per layer one
     store, then per sequence a host read of its context length and one
     gather each of K and V.  The packed metadata is the same as the hip
     step's (packed once, outside the timed region; the reference packs on
-    the host).  The outputs are dropped where SDPA would consume them."""
+    the host).  The outputs are dropped where SDPA would consume them.
+    ``ref`` is the backend driven (default: the torch restatement of the
+    reference pytorch backend; the hip backend gives the step that switching
+    paged_kv_backend alone, with SDPA unchanged, would run)."""
     import torch
 
-    ref = reference_backend()
+    ref = ref if ref is not None else reference_backend()
     ctx = packer.pack_decode(batch)
     torch.cuda.synchronize()
 
