@@ -127,6 +127,15 @@ def _require_contiguous_cache(what: str, *caches: torch.Tensor) -> None:
             raise ValueError(f"{what} requires contiguous [blocks, block, kv_heads, head_dim] caches")
 
 
+def _int32_index(what: str, name: str, index: torch.Tensor) -> torch.Tensor:
+    """An index tensor as the kernels read it: int32 (a direct op call with
+    another dtype raises, as the reference op's typed data_ptr<int32_t> does)
+    and contiguous (a strided view is compacted on the device)."""
+    if index.dtype != torch.int32:
+        raise RuntimeError(f"{what}: {name} must be int32, got {index.dtype}")
+    return index if index.is_contiguous() else index.contiguous()
+
+
 def _plan_capacity(total: int, num_seqs: int, block_size: int, row_elems: int, code: int) -> int:
     return int(
         _lib.load_library().nkv_gather_plan_capacity(total, num_seqs, block_size, row_elems, code)
@@ -138,6 +147,7 @@ def _store_impl(key, value, key_cache, value_cache, slot_mapping) -> None:
     _require_contiguous_cache("paged KV HIP Store", key_cache, value_cache)
     if key.dtype != value.dtype or key.dtype != key_cache.dtype or key.dtype != value_cache.dtype:
         raise RuntimeError("Paged KV HIP Store dtype mismatch")
+    slot_mapping = _int32_index("Paged KV HIP Store", "slot_mapping", slot_mapping)
     num_tokens = key.shape[0]
     if num_tokens == 0:
         return
@@ -170,6 +180,7 @@ def _store_impl(key, value, key_cache, value_cache, slot_mapping) -> None:
 def _gather_impl(cache, block_table, sequence_length: int) -> torch.Tensor:
     device = _require_device("paged KV HIP Gather", cache, block_table)
     _require_contiguous_cache("paged KV HIP Gather", cache)
+    block_table = _int32_index("Paged KV HIP Gather", "block_table", block_table)
     num_blocks, block_size, heads, head_dim = cache.shape
     out = torch.empty((sequence_length, heads, head_dim), dtype=cache.dtype, device=device)
     if sequence_length == 0:

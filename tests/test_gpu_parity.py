@@ -107,6 +107,33 @@ def test_registered_ops_dispatch_to_hip(backend, gpu_device):
     np.testing.assert_array_equal(words(v_out), expect_v)
 
 
+def test_registered_ops_index_dtype_and_strides(backend, gpu_device):
+    """A direct op call (no backend validators in front) with int64 slots or
+    block table raises, as the reference op's typed data_ptr<int32_t> does;
+    strided int32 index views are read by element, not by raw memory."""
+    backend._load()
+    torch.manual_seed(43)
+    key = torch.randn(6, 2, 64, device=gpu_device, dtype=torch.bfloat16)
+    value = torch.randn_like(key)
+    kc = torch.full((4, 8, 2, 64), -3, device=gpu_device, dtype=torch.bfloat16)
+    vc = torch.full_like(kc, -3)
+    with pytest.raises(RuntimeError, match="int32"):
+        torch.ops.nanovllm_paged_kv.store(key, value, kc, vc,
+                                          torch.arange(6, device=gpu_device, dtype=torch.int64))
+    with pytest.raises(RuntimeError, match="int32"):
+        torch.ops.nanovllm_paged_kv.gather(kc, torch.tensor([3, 1], device=gpu_device), 9)
+    # every other element of a 12-element buffer: slots [5, 30, -1, 9, 2, 17]
+    wide = torch.tensor([5, 0, 30, 0, -1, 0, 9, 0, 2, 0, 17, 0], device=gpu_device, dtype=torch.int32)
+    slots = wide[::2]
+    hk, hv = oracle_store(key, value, kc, vc, slots.contiguous())
+    torch.ops.nanovllm_paged_kv.store(key, value, kc, vc, slots)
+    np.testing.assert_array_equal(words(kc), hk)
+    np.testing.assert_array_equal(words(vc), hv)
+    table = torch.tensor([[3, 7], [1, 7], [0, 7]], device=gpu_device, dtype=torch.int32)[:, 0]
+    np.testing.assert_array_equal(words(torch.ops.nanovllm_paged_kv.gather(kc, table, 19)),
+                                  oracle.gather(hk, np.array([3, 1, 0]), 19))
+
+
 def test_store_of_head_strided_views(backend, gpu_device):
     """A view strided between heads (kv[:, :, :128] of a [T, H, 256]
     tensor) passes the validators, which only ask for a contiguous last
