@@ -206,6 +206,11 @@ def _build_plan_impl(
     row_elems: int, dtype: torch.dtype,
 ) -> torch.Tensor:
     device = _require_device("paged KV HIP plan", block_tables, cu_seqlens_k)
+    cu_seqlens_k = _int32_index("Paged KV HIP plan", "cu_seqlens_k", cu_seqlens_k)
+    if block_tables.dtype != torch.int32:
+        raise RuntimeError(f"Paged KV HIP plan: block_tables must be int32, got {block_tables.dtype}")
+    if block_tables.ndim == 2 and block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()  # the kernel walks a row through stride(0) only
     num_seqs = cu_seqlens_k.numel() - 1
     code = dtype_code(dtype)
     capacity = _plan_capacity(total_tokens, num_seqs, block_size, row_elems, code)

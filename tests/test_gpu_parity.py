@@ -132,6 +132,20 @@ def test_registered_ops_index_dtype_and_strides(backend, gpu_device):
     table = torch.tensor([[3, 7], [1, 7], [0, 7]], device=gpu_device, dtype=torch.int32)[:, 0]
     np.testing.assert_array_equal(words(torch.ops.nanovllm_paged_kv.gather(kc, table, 19)),
                                   oracle.gather(hk, np.array([3, 1, 0]), 19))
+    # gather_varlen: int64 tables or lengths raise; a column-strided table is read by element
+    cu = torch.tensor([0, 19, 24], device=gpu_device, dtype=torch.int32)
+    tables = torch.tensor([[3, 1, 0], [2, -1, -1]], device=gpu_device, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="int32"):
+        torch.ops.nanovllm_paged_kv.gather_varlen(kc, vc, tables.long(), cu, 24)
+    with pytest.raises(RuntimeError, match="int32"):
+        torch.ops.nanovllm_paged_kv.gather_varlen(kc, vc, tables, cu.long(), 24)
+    strided = torch.stack([tables, torch.full_like(tables, 7)], dim=2).reshape(2, 6)[:, ::2]
+    assert strided.stride(1) == 2 and torch.equal(strided, tables)
+    k_out, v_out = torch.ops.nanovllm_paged_kv.gather_varlen(kc, vc, strided, cu, 24)
+    np.testing.assert_array_equal(words(k_out), np.concatenate(
+        [oracle.gather(hk, np.array([3, 1, 0]), 19), oracle.gather(hk, np.array([2]), 5)]))
+    np.testing.assert_array_equal(words(v_out), np.concatenate(
+        [oracle.gather(hv, np.array([3, 1, 0]), 19), oracle.gather(hv, np.array([2]), 5)]))
 
 
 def test_store_of_head_strided_views(backend, gpu_device):
