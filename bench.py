@@ -199,7 +199,7 @@ def main(argv=None) -> int:
 
         log("[bench] rocprofv3 kernel trace of the decode step on this host")
         same_host_trace = trace_kernel_here("decode_step", "gather_planned_kernel", replay=10,
-                                            settle_s=args.settle_s, timeout_s=150)
+                                            settle_s=args.settle_s, timeout_s=240, echo=True)
         log(f"[bench] same-host trace: {same_host_trace.get('median_us', same_host_trace.get('error'))}")
 
     import numpy as np

@@ -105,7 +105,8 @@ def collection_plan(case: str, out: Path, *, replay: int = 20, counter_replay: i
 
 
 def trace_kernel_here(case: str, kernel_prefix: str, *, replay: int = 10, timeout_s: int = 300,
-                      bench: str | Path | None = None, settle_s: float | None = None) -> dict:
+                      bench: str | Path | None = None, settle_s: float | None = None,
+                      echo: bool = False) -> dict:
     """Run ``trace_command(case)`` as a child process on this host (in a
     scratch directory under /tmp, TMPDIR=/tmp, the program straight after
     ``--``) and return the trace statistics of the first kernel whose short
@@ -113,10 +114,12 @@ def trace_kernel_here(case: str, kernel_prefix: str, *, replay: int = 10, timeou
     command.  Never raises: a missing profiler, a time-out or output without
     that kernel gives ``{"error": ...}``.  rocprofv3 may exit non-zero after
     the program finished and wrote its trace; the trace is used whenever the
-    replay printed its last line."""
+    replay printed its last line.  ``echo`` forwards the child's output to
+    stderr line by line as it arrives."""
     import shutil
     import signal
     import tempfile
+    import threading
 
     rocprof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3"
                                              if os.path.exists("/opt/rocm/bin/rocprofv3") else None)
@@ -130,12 +133,25 @@ def trace_kernel_here(case: str, kernel_prefix: str, *, replay: int = 10, timeou
         env = dict(os.environ, TMPDIR="/tmp")
         proc = subprocess.Popen(command, cwd="/tmp", env=env, stdout=subprocess.PIPE,
                                 stderr=subprocess.STDOUT, text=True, start_new_session=True)
+        lines: list[str] = []
+
+        def forward() -> None:  # the child's lines as they come, so a slow start shows
+            for line in proc.stdout:
+                lines.append(line)
+                if echo:
+                    print(f"[trace] {line.rstrip()}", file=sys.stderr, flush=True)
+
+        reader = threading.Thread(target=forward, daemon=True)
+        reader.start()
         try:
-            output, _ = proc.communicate(timeout=timeout_s)
+            proc.wait(timeout=timeout_s)
         except subprocess.TimeoutExpired:
             os.killpg(proc.pid, signal.SIGKILL)
-            proc.communicate()
+            proc.wait()
+            reader.join(timeout=10)
             return {"error": f"trace of {case} did not finish in {timeout_s} s"}
+        reader.join(timeout=10)
+        output = "".join(lines)
         if "profile replay complete" not in output:
             tail = output.strip().splitlines()[-3:]
             return {"error": f"replay of {case} did not complete (exit {proc.returncode}): "

@@ -246,3 +246,13 @@ def test_same_host_roofline_record():
     assert got["events_over_trace_mean"] == pytest.approx(1160 / 1150, abs=1e-4)
     assert bench.same_host_roofline({"error": "x"}, 1, 1.0) == {"error": "x"}
     assert bench.same_host_roofline(None, 1, 1.0) is None
+
+
+def test_trace_on_this_host_echoes_the_child(tmp_path, monkeypatch, capsys):
+    """With echo the child's lines reach stderr as they arrive, so a slow
+    child (a cold first import) is visible while the bench waits for it."""
+    fake_rocprof(tmp_path, monkeypatch, n=3)
+    got = profiling.trace_kernel_here("decode_step", "gather_planned_kernel", replay=10,
+                                      timeout_s=60, echo=True)
+    assert "error" not in got
+    assert "[trace] profile replay complete: decode_step" in capsys.readouterr().err
