@@ -180,52 +180,47 @@ int nkv_gather_varlen(const void* key_cache, const void* value_cache,
  * of request i at cu_seqlens_k[i] + p, as nkv_gather_varlen does.  The
  * caches are updated exactly as nkv_store updates them.
  *
- * Exactness condition (what the reference's packing produces,
- * model_runner.py:757-820): no two tokens share a slot, a token's slot is
- * -1 or the table-derived slot of its own position, and no block receives
- * new rows from two requests.  A token whose slot is -1 or differs is
- * stored as given, and every output row of its position (its own, and
- * other requests' cached rows there) is read from the cache, as the gather
- * finds it (the reference's store already forbids duplicate slots,
- * attention.py:24-25).
+ * Exactness condition (what the reference's packing and scheduling
+ * produce): no two tokens share a slot, a token's slot is -1 or the
+ * table-derived slot of its own position (model_runner.py:757-820), and no
+ * request's cached prefix, positions [0, Lk - Lq), holds a row that a token
+ * of this call stores.  The reference guarantees the last: a block enters
+ * the prefix cache only after the step that filled it (Scheduler.postprocess
+ * -> BlockManager.hash_blocks, nanovllm/engine/scheduler.py:196-200,
+ * block_manager.py:229-258), so a request of a step never finds its prefix
+ * in rows that step writes.  A token whose slot is -1 or differs is stored
+ * as given, and its output row is read from the cache row of its position,
+ * as the gather finds it (the reference's store already forbids duplicate
+ * slots, attention.py:24-25).  A batch that breaks the last condition gets
+ * unspecified values in the output rows concerned (never an access outside
+ * the buffers); nkv_store followed by nkv_gather_varlen handles it.
  *
  * Replaces: the store call of Attention.forward (nanovllm/layers/
  *   attention.py:87-93) together with the per-request gathers of
  *   SDPAAttention's prefill (attention.py:250-259), as one launch.
  *
- * Requests of one step may share blocks (a request's cached prefix can sit
- * in blocks another request of the step is filling, since the reference
- * registers a block's hash at allocation, block_manager.py:159-214).  The
- * plan records which request writes which block in this step in a
- * caller-owned writer map (nkv_store_gather_map_bytes: one int64 per cache
- * block, zeroed once before its first use, never cleared after), tagged
- * with step_tag; cached rows written in this step are taken from the
- * writing token's K/V row.  Give each plan of a map a new nonzero
- * step_tag (a counter; zero the map again if it wraps).
- *
- * nkv_store_gather_plan_bytes: bytes of the per-step plan (32 per chunk of
+ * nkv_store_gather_plan_bytes: bytes of the per-step plan (16 per chunk of
  *   cached rows, 8 per token).
- * nkv_build_store_gather_plan: builds it on the device (two launches) from
+ * nkv_build_store_gather_plan: builds it on the device (one launch) from
  *   block_tables [num_seqs, table_stride], cu_seqlens_q and cu_seqlens_k
  *   (num_seqs at most NKV_MAX_PACK_SEQS); num_tokens is the step's rows of
  *   key / value / slot_mapping (cu_seqlens_q[num_seqs]) and out_rows its
- *   context rows (cu_seqlens_k[num_seqs]).  One plan serves every layer;
- *   nkv_store_gather must be given the same num_tokens, out_rows and
- *   geometry.
- * nkv_store_gather: the launch.  Every index the kernel reads from device
+ *   context rows (cu_seqlens_k[num_seqs]).  One plan serves every layer.
+ * nkv_store_gather: the launch.  plan_bytes must be exactly what
+ *   nkv_store_gather_plan_bytes returns for this call's num_tokens,
+ *   out_rows, num_seqs and geometry (a plan built for other counts is
+ *   rejected with NKV_E_CAPACITY).  Every index the kernel reads from device
  *   memory is bounded by the buffers, whatever the plan holds.
  */
 int64_t nkv_store_gather_plan_bytes(int64_t num_tokens, int64_t total_rows,
                                     int64_t num_seqs, int64_t block_size,
                                     int64_t row_elems, int32_t dtype);
-int64_t nkv_store_gather_map_bytes(int64_t num_blocks);
 int nkv_build_store_gather_plan(const int32_t* block_tables, int64_t table_stride,
                                 const int32_t* cu_seqlens_q,
                                 const int32_t* cu_seqlens_k, int64_t num_seqs,
                                 int64_t num_tokens, int64_t out_rows,
                                 int64_t block_size, int64_t row_elems,
-                                int64_t num_blocks, int32_t dtype, void* writer_map,
-                                int64_t map_bytes, uint32_t step_tag, void* plan,
+                                int64_t num_blocks, int32_t dtype, void* plan,
                                 int64_t plan_bytes, void* stream);
 int nkv_store_gather(const void* key, const void* value, void* key_cache,
                      void* value_cache, const int32_t* slot_mapping,

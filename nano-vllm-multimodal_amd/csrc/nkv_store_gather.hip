@@ -15,8 +15,8 @@
 //    its cache slot (the store) and to its context row of the gathered
 //    output (the gather);
 //  * cached-row workgroups copy the cached prefixes, positions [0, Lk - Lq),
-//    from the cache to the output, driven by chunk entries as in the varlen
-//    gather.
+//    from the cache to the output, driven by chunk entries exactly as the
+//    varlen gather's plan drives its copies.
 // That is what store followed by gather produces whenever every token's
 // slot is -1 or the table-derived slot of its position and no slot repeats,
 // which is how the reference packs them (model_runner.py:757-820) and what
@@ -25,21 +25,23 @@
 // table-derived slot) is stored as given, and its output row is read from
 // the cache row of its position instead, as the gather would find it.
 //
-// Requests of one step may share blocks: the reference registers a block's
-// prefix hash when it allocates the block (block_manager.py:159-214), so a
-// request can find its cached prefix in blocks another request of the same
-// step is only now filling.  Store-then-gather reads those rows after the
-// store; here they would be read while being written.  So the plan records,
-// in a caller-owned map of one int64 per cache block tagged with the step,
-// which request writes which block in this step, and a cached-prefix chunk
-// whose rows are written in this step takes them from the writing token's
-// K/V row instead of the cache.
+// No cached-prefix row is written in the same step.  A request's cached
+// prefix is either its own earlier chunks or blocks it hit in the prefix
+// cache, and a block enters the prefix cache only after the step that
+// filled it: Scheduler.postprocess calls BlockManager.hash_blocks once the
+// model has run (nanovllm/engine/scheduler.py:196-200), hash_blocks is the
+// one place a hash is registered (block_manager.py:229-258), and
+// can_allocate / allocate only look hashes up (block_manager.py:119-198).
+// So the cached-row copies and the new-row stores of one launch touch
+// disjoint cache rows, and the two kinds of workgroups need no ordering.  A
+// batch that breaks this (a request reading, as cached prefix, rows another
+// request of the same call stores) gets unspecified values in those output
+// rows, never an access outside the buffers; store then gather handles it.
 //
-// The plan (two launches per step, shared by all layers and by K and V):
-//  * per token t, {output row, table-derived slot}; the first new token of
-//    each (request, block) records the block's writer in the map;
-//  * per chunk of a cached prefix, {source row, output row, rows, request}
-//    and {token of chunk row 0 if it were new, new-row range [lo, hi)}.
+// The plan (one launch per step, shared by all layers and by K and V):
+//  * per token t, {output row, table-derived slot} (-1 where there is none);
+//  * per chunk of a cached prefix, {source row, output row, rows, request},
+//    the varlen gather's entry layout.
 // Launch shape and cache policy are those of the store and gather
 // (128-thread workgroups of ~4 KiB of one tensor, blockIdx.y = K or V, one
 // batch of 16-byte words per lane, non-temporal accesses).
@@ -51,10 +53,6 @@ namespace {
 constexpr int kSgThreads = 128;
 constexpr int kSgWgBytes = 4096;
 constexpr int kSgPlanThreads = 1024;
-constexpr int kSgMetaThreads = 256;
-constexpr int kWriterSeqBits = 12;    // NKV_MAX_PACK_SEQS = 4096 requests
-constexpr int kWriterBlockBits = 20;  // logical blocks per request
-static_assert((1 << kWriterSeqBits) >= NKV_MAX_PACK_SEQS, "writer map request field too narrow");
 
 template <int W>
 constexpr int sg_batch() {
@@ -76,17 +74,48 @@ __device__ __forceinline__ int32_t owner_in(const int32_t* __restrict__ cu, int3
   return lo;
 }
 
-// Plan, first launch: meta[t] = {output row, table-derived slot} of every
-// token (-1 where there is none), and the map entry of every block that
-// receives new rows in this step: tag << 32 | request << 20 | logical block.
-__global__ __launch_bounds__(kSgMetaThreads) void store_gather_meta_kernel(
+// The whole plan in one launch: every workgroup rescans the per-request
+// chunk counts of the cached prefixes in LDS, then the grid strides over
+// the chunk entries and over the tokens.
+__global__ __launch_bounds__(kSgPlanThreads) void store_gather_plan_kernel(
     const int32_t* __restrict__ tables, int64_t table_stride,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, int32_t num_seqs,
-    int32_t num_tokens, int32_t block_size, int64_t num_blocks, int64_t out_rows,
-    uint32_t tag, int64_t* __restrict__ writers, int2* __restrict__ meta) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSgMetaThreads;
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kSgMetaThreads + threadIdx.x;
-       e < num_tokens; e += stride) {
+    int32_t num_tokens, int32_t block_size, int32_t chunk_rows, int64_t num_blocks,
+    int64_t out_rows, int2* __restrict__ meta, int4* __restrict__ entries, int64_t capacity) {
+  extern __shared__ int32_t s_mem[];
+  int32_t* s_first = s_mem;                 // [num_seqs + 1]
+  int32_t* s_tmp = s_first + num_seqs + 1;  // [kSgPlanThreads / 64 + 1]
+  lds_exclusive_scan<kSgPlanThreads>(
+      num_seqs,
+      [&](int32_t i) {
+        const int32_t cached = (cu_k[i + 1] - cu_k[i]) - (cu_q[i + 1] - cu_q[i]);
+        return cached > 0 ? (cached + chunk_rows - 1) / chunk_rows : 0;
+      },
+      s_first, s_tmp);
+  const int64_t total = s_first[num_seqs];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSgPlanThreads;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kSgPlanThreads + threadIdx.x;
+  for (int64_t k = first; k < capacity; k += stride) {
+    int4 entry = make_int4(0, 0, 0, 0);
+    if (k < total) {
+      const int32_t i = owner_of(s_first, num_seqs, static_cast<int32_t>(k));
+      const int32_t row0 = (static_cast<int32_t>(k) - s_first[i]) * chunk_rows;
+      const int32_t cached = (cu_k[i + 1] - cu_k[i]) - (cu_q[i + 1] - cu_q[i]);
+      int64_t nrows = min(chunk_rows, cached - row0);
+      const int64_t dst = static_cast<int64_t>(cu_k[i]) + row0;
+      if (dst < 0 || dst >= out_rows) nrows = 0;
+      if (dst + nrows > out_rows) nrows = out_rows - dst;
+      const int64_t logical = row0 / block_size;
+      int32_t src = -1;
+      if (logical < table_stride) {
+        const int32_t block = tables[i * table_stride + logical];
+        if (block >= 0 && block < num_blocks) src = block * block_size + row0 % block_size;
+      }
+      entry = make_int4(src, static_cast<int32_t>(dst), static_cast<int32_t>(nrows), i);
+    }
+    entries[k] = entry;
+  }
+  for (int64_t e = first; e < num_tokens; e += stride) {
     const int32_t t = static_cast<int32_t>(e);
     int2 m = make_int2(-1, -1);
     if (num_seqs > 0 && t >= cu_q[0] && t < cu_q[num_seqs]) {
@@ -100,14 +129,7 @@ __global__ __launch_bounds__(kSgMetaThreads) void store_gather_meta_kernel(
         const int64_t logical = p / block_size;
         if (logical < table_stride) {
           const int32_t block = tables[i * table_stride + logical];
-          if (block >= 0 && block < num_blocks) {
-            m.y = block * block_size + p % block_size;
-            if ((p % block_size == 0 || t == q0) && logical < (int64_t{1} << kWriterBlockBits)) {
-              writers[block] = static_cast<int64_t>(
-                  (static_cast<uint64_t>(tag) << 32) |
-                  (static_cast<uint64_t>(i) << kWriterBlockBits) | static_cast<uint64_t>(logical));
-            }
-          }
+          if (block >= 0 && block < num_blocks) m.y = block * block_size + p % block_size;
         }
       }
     }
@@ -115,108 +137,54 @@ __global__ __launch_bounds__(kSgMetaThreads) void store_gather_meta_kernel(
   }
 }
 
-// Plan, second launch: two int4 per chunk of cached rows (positions
-// [0, Lk - Lq) of each request, chunk_rows rows inside one block):
-// {source row (-1: invalid block), output row, rows, request} and {token of
-// the chunk's first row if it were new, new-row range [lo, hi) within the
-// chunk, 0}.  Rows in [lo, hi) are written in this step by another request
-// (its map entry carries this step's tag) and come from that token's row
-// when that token's slot is the row.
-__global__ __launch_bounds__(kSgPlanThreads) void store_gather_chunk_kernel(
-    const int32_t* __restrict__ tables, int64_t table_stride,
-    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, int32_t num_seqs,
-    int32_t block_size, int32_t chunk_rows, int64_t num_blocks, int64_t out_rows, uint32_t tag,
-    const int64_t* __restrict__ writers, int4* __restrict__ entries, int64_t capacity) {
-  extern __shared__ int32_t s_mem[];
-  int32_t* s_first = s_mem;                 // [num_seqs + 1]
-  int32_t* s_tmp = s_first + num_seqs + 1;  // [kSgPlanThreads / 64 + 1]
-  lds_exclusive_scan<kSgPlanThreads>(
-      num_seqs,
-      [&](int32_t i) {
-        const int32_t cached = (cu_k[i + 1] - cu_k[i]) - (cu_q[i + 1] - cu_q[i]);
-        return cached > 0 ? (cached + chunk_rows - 1) / chunk_rows : 0;
-      },
-      s_first, s_tmp);
-  const int64_t total = s_first[num_seqs];
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSgPlanThreads;
-  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kSgPlanThreads + threadIdx.x; k < capacity;
-       k += stride) {
-    int4 head = make_int4(0, 0, 0, 0);
-    int4 tail = make_int4(0, 0, 0, 0);
-    if (k < total) {
-      const int32_t i = owner_of(s_first, num_seqs, static_cast<int32_t>(k));
-      const int32_t row0 = (static_cast<int32_t>(k) - s_first[i]) * chunk_rows;
-      const int32_t cached = (cu_k[i + 1] - cu_k[i]) - (cu_q[i + 1] - cu_q[i]);
-      int64_t nrows = min(chunk_rows, cached - row0);
-      const int64_t dst = static_cast<int64_t>(cu_k[i]) + row0;
-      if (dst < 0 || dst >= out_rows) nrows = 0;
-      if (dst + nrows > out_rows) nrows = out_rows - dst;
-      const int64_t logical = row0 / block_size;
-      const int32_t offset = row0 % block_size;
-      int32_t src = -1;
-      if (logical < table_stride) {
-        const int32_t block = tables[i * table_stride + logical];
-        if (block >= 0 && block < num_blocks) {
-          src = block * block_size + offset;
-          const uint64_t w = static_cast<uint64_t>(writers[block]);
-          const int32_t wi = static_cast<int32_t>((w >> kWriterBlockBits) & ((1u << kWriterSeqBits) - 1));
-          if (static_cast<uint32_t>(w >> 32) == tag && wi < num_seqs) {
-            const int64_t wl = static_cast<int64_t>(w & ((1u << kWriterBlockBits) - 1));
-            const int32_t wq0 = cu_q[wi];
-            const int32_t wlk = cu_k[wi + 1] - cu_k[wi];
-            const int32_t wstart = wlk - (cu_q[wi + 1] - wq0);
-            // the writer's new positions inside this block, relative to the chunk
-            const int64_t first = wl * block_size + offset;  // writer position of chunk row 0
-            const int64_t lo = max<int64_t>(0, min<int64_t>(nrows, wstart - first));
-            const int64_t hi = max<int64_t>(lo, min<int64_t>(nrows, wlk - first));
-            if (lo < hi) {
-              tail = make_int4(static_cast<int32_t>(wq0 + (first - wstart)), static_cast<int32_t>(lo),
-                               static_cast<int32_t>(hi), 0);
-            }
-          }
-        }
-      }
-      head = make_int4(src, static_cast<int32_t>(dst), static_cast<int32_t>(nrows), i);
-    }
-    entries[2 * k] = head;
-    entries[2 * k + 1] = tail;
+// Grid position b holds a cached-row workgroup when
+// umulhi(b + 1, spread) > umulhi(b, spread), spread = ceil(C * 2^32 / G) for
+// C cached-row workgroups of G (C < G): umulhi(b, spread) counts the cached
+// workgroups before b, steps by 0 or 1 and reaches exactly C at b = G, so
+// the two kinds are spread evenly over the grid and every index of each
+// kind occurs once.  The write-heavy new rows (one read, two writes) and the
+// cached copies (one read, one write) then share the launch instead of
+// running one after the other.  With no new-row workgroups (C = G) every
+// position is cached.  32-bit multiplies only (two scalar mul_hi per
+// workgroup), no division.
+__device__ __forceinline__ bool sg_is_cached(uint32_t b, uint32_t spread, int32_t new_wgs,
+                                             uint32_t* index) {
+  if (new_wgs == 0) {
+    *index = b;
+    return true;
   }
+  const uint32_t before = __umulhi(b, spread);
+  if (__umulhi(b + 1, spread) > before) {
+    *index = before;
+    return true;
+  }
+  *index = b - before;
+  return false;
 }
 
-// new_wgs workgroups move rows_per_wg consecutive tokens of K or V each;
-// the others copy one sub-chunk of sub_rows rows of a cached-row chunk.  The
-// two kinds are spread evenly over the grid: workgroup b copies cached rows
-// when floor((b + 1) C / T) > floor(b C / T) (C cached-row workgroups of T),
-// so the write-heavy new rows (one read, two writes) and the cached copies
-// (one read, one write) share the launch instead of running one after the
-// other (narrow-row step 37.6-38.0 -> 35.6-35.9 us; the chunked-prefill step
-// unchanged).  Every index read from device memory is re-checked against the
-// buffers (slots against num_slots, output rows against out_rows, chunk
-// sources against the cache, tokens against num_tokens), so no plan can make
-// the launch leave them.
+// Every index read from device memory is re-checked against the buffers
+// (slots against num_slots, output rows against out_rows, chunk sources
+// against the cache), so no plan can make the launch leave them.
 template <int W>
 __global__ __launch_bounds__(kSgThreads) void store_gather_kernel(
     const uint8_t* __restrict__ key, const uint8_t* __restrict__ value,
     uint8_t* __restrict__ key_cache, uint8_t* __restrict__ value_cache,
     const int32_t* __restrict__ slot_mapping, const int2* __restrict__ meta,
     int32_t num_tokens, int64_t key_stride, int64_t value_stride, int64_t row_bytes,
-    int32_t row_words, int32_t rows_per_wg, int64_t num_slots, int32_t new_wgs,
+    int32_t row_words, int32_t rows_per_wg, int64_t num_slots, int32_t new_wgs, uint32_t spread,
     const int4* __restrict__ entries, int32_t subs_per_entry, int32_t sub_rows,
     int64_t out_rows, uint8_t* __restrict__ key_out, uint8_t* __restrict__ value_out) {
   using T = typename Word<W>::type;
   const bool second = blockIdx.y != 0;
   uint8_t* const cache = second ? value_cache : key_cache;
   uint8_t* const out = second ? value_out : key_out;
-  const uint8_t* const src = second ? value : key;
-  const int64_t stride = second ? value_stride : key_stride;
-  const int64_t total_wgs = gridDim.x;
-  const int64_t cached_wgs = total_wgs - new_wgs;
-  const int64_t b = blockIdx.x;
-  const int64_t cached_before = b * cached_wgs / total_wgs;  // cached-row workgroups before b
-  if ((b + 1) * cached_wgs / total_wgs == cached_before) {     // a new-row workgroup
+  uint32_t x;
+  if (!sg_is_cached(blockIdx.x, spread, new_wgs, &x)) {
+    const uint8_t* const src = second ? value : key;
+    const int64_t stride = second ? value_stride : key_stride;
     constexpr int U = sg_batch<W>();
-    // b - cached_before < new_wgs, so t0 < num_tokens by the grid
-    const int32_t t0 = static_cast<int32_t>(b - cached_before) * rows_per_wg;
+    // x < new_wgs, so t0 < num_tokens by the grid
+    const int32_t t0 = static_cast<int32_t>(x) * rows_per_wg;
     const int32_t nwords = min(rows_per_wg, num_tokens - t0) * row_words;
     for (int32_t base = 0; base < nwords; base += U * kSgThreads) {
       int32_t row[U], col[U], slot[U];
@@ -254,46 +222,23 @@ __global__ __launch_bounds__(kSgThreads) void store_gather_kernel(
     }
     return;
   }
-  const int32_t x = static_cast<int32_t>(cached_before);  // this workgroup's cached-row index
-  const int32_t e = x / subs_per_entry;
-  const int32_t row_off = (x - e * subs_per_entry) * sub_rows;
-  const int4 head = entries[2 * e];
-  if (head.z <= row_off || head.y < 0 || static_cast<int64_t>(head.y) + head.z > out_rows) return;
-  const int4 tail = entries[2 * e + 1];
-  const int32_t nrows = min(sub_rows, head.z - row_off);
-  T* d = reinterpret_cast<T*>(out + (static_cast<int64_t>(head.y) + row_off) * row_bytes);
+  const int32_t e = static_cast<int32_t>(x) / subs_per_entry;
+  const int32_t row_off = (static_cast<int32_t>(x) - e * subs_per_entry) * sub_rows;
+  const int4 entry = entries[e];
+  if (entry.z <= row_off || entry.y < 0 || static_cast<int64_t>(entry.y) + entry.z > out_rows) return;
+  const int32_t nrows = min(sub_rows, entry.z - row_off);
+  T* d = reinterpret_cast<T*>(out + (static_cast<int64_t>(entry.y) + row_off) * row_bytes);
   const auto nwords = static_cast<int32_t>(nrows * row_bytes / W);
-  const bool cache_ok = head.x >= 0 && static_cast<int64_t>(head.x) + head.z <= num_slots;
-  const T* s = reinterpret_cast<const T*>(cache + (static_cast<int64_t>(cache_ok ? head.x : 0) + row_off) *
-                                          row_bytes);
-  const int32_t lo = tail.y - row_off, hi = tail.z - row_off;  // new rows, relative to row_off
-  if (lo >= nrows || hi <= 0 || lo >= hi) {                     // none here: a plain copy
-    for (int32_t i = threadIdx.x; i < nwords; i += kSgThreads) {
-      store_stream(d + i, cache_ok ? load_stream(s + i) : T{});
-    }
+  if (entry.x < 0 || static_cast<int64_t>(entry.x) + entry.z > num_slots) {
+    for (int32_t i = threadIdx.x; i < nwords; i += kSgThreads) store_stream(d + i, T{});
     return;
   }
-  for (int32_t i = threadIdx.x; i < nwords; i += kSgThreads) {
-    const int32_t r = i / row_words;
-    const int32_t c = i - r * row_words;
-    T o = T{};
-    const int64_t t = static_cast<int64_t>(tail.x) + row_off + r;
-    // A row of another request's new range: the store writes it from token
-    // t, unless t's slot is not this cache row (-1 or elsewhere), in which
-    // case the row keeps its cache contents.
-    const bool fresh = r >= lo && r < hi && t >= 0 && t < num_tokens && cache_ok &&
-                       slot_mapping[t] == head.x + row_off + r;
-    if (fresh) {
-      o = load_stream(reinterpret_cast<const T*>(src + t * stride) + c);
-    } else if (cache_ok) {
-      o = load_stream(s + i);
-    }
-    store_stream(d + i, o);
-  }
+  const T* s = reinterpret_cast<const T*>(cache + (static_cast<int64_t>(entry.x) + row_off) * row_bytes);
+  for (int32_t i = threadIdx.x; i < nwords; i += kSgThreads) store_stream(d + i, load_stream(s + i));
 }
 
-// Plan layout: num_tokens int2 meta (rounded up to 16 bytes), then two
-// int4 per chunk.
+// Plan layout: num_tokens int2 meta (rounded up to 16 bytes), then one int4
+// per chunk.
 int64_t meta_bytes(int64_t num_tokens) { return (num_tokens * 8 + 15) / 16 * 16; }
 
 int64_t divisor_at_most(int64_t rows, int64_t target) {
@@ -322,6 +267,20 @@ int check_sg_geometry(const char* what, int64_t num_tokens, int64_t num_seqs, in
   return NKV_OK;
 }
 
+// A plan is laid out for one (num_tokens, out_rows, num_seqs, geometry):
+// its size must be the one nkv_store_gather_plan_bytes gives for them, so a
+// plan built for other counts is rejected instead of read at the wrong
+// offsets.
+int check_plan_bytes(const char* what, int64_t plan_bytes, int64_t need) {
+  if (need > 0 ? plan_bytes != need : plan_bytes < 0) {
+    return nkv_fail(NKV_E_CAPACITY,
+                    "%s: plan of %lld bytes, these token/context counts and geometry need "
+                    "exactly %lld (build the plan for the same counts)",
+                    what, static_cast<long long>(plan_bytes), static_cast<long long>(need));
+  }
+  return NKV_OK;
+}
+
 template <int W>
 int launch_store_gather(const void* key, const void* value, void* key_cache, void* value_cache,
                         const int32_t* slots, const int2* meta, int32_t num_tokens, int64_t ks,
@@ -335,15 +294,21 @@ int launch_store_gather(const void* key, const void* value, void* key_cache, voi
   const int64_t new_wgs = (num_tokens + rows_per_wg - 1) / rows_per_wg;
   const int64_t sub_rows = divisor_at_most(chunk_rows, kSgWgBytes / row_bytes);
   const int64_t subs = chunk_rows / sub_rows;
-  const int64_t wgs = new_wgs + capacity * subs;
+  const int64_t cached_wgs = capacity * subs;
+  const int64_t wgs = new_wgs + cached_wgs;
   if (wgs == 0) return NKV_OK;
-  if (wgs > INT32_MAX) return nkv_fail(NKV_E_INVALID, "nkv_store_gather: launch too large");
+  if (wgs >= INT32_MAX) return nkv_fail(NKV_E_INVALID, "nkv_store_gather: launch too large");
+  // ceil(cached * 2^32 / wgs) < 2^32 whenever new_wgs > 0 (see sg_is_cached)
+  const uint32_t spread =
+      new_wgs > 0 ? static_cast<uint32_t>(((static_cast<uint64_t>(cached_wgs) << 32) + wgs - 1) /
+                                          static_cast<uint64_t>(wgs))
+                  : 0u;
   store_gather_kernel<W><<<dim3(static_cast<unsigned>(wgs), 2), dim3(kSgThreads), 0, stream>>>(
       static_cast<const uint8_t*>(key), static_cast<const uint8_t*>(value),
       static_cast<uint8_t*>(key_cache), static_cast<uint8_t*>(value_cache), slots, meta,
       num_tokens, ks, vs, row_bytes, static_cast<int32_t>(row_words),
-      static_cast<int32_t>(rows_per_wg), num_slots, static_cast<int32_t>(new_wgs), entries,
-      static_cast<int32_t>(subs), static_cast<int32_t>(sub_rows), out_rows,
+      static_cast<int32_t>(rows_per_wg), num_slots, static_cast<int32_t>(new_wgs), spread,
+      entries, static_cast<int32_t>(subs), static_cast<int32_t>(sub_rows), out_rows,
       static_cast<uint8_t*>(key_out), static_cast<uint8_t*>(value_out));
   return nkv_check_launch("nkv_store_gather");
 }
@@ -358,11 +323,7 @@ extern "C" int64_t nkv_store_gather_plan_bytes(int64_t num_tokens, int64_t total
   const int64_t capacity =
       nkv_gather_plan_capacity(total_rows, num_seqs, block_size, row_elems, dtype);
   if (capacity <= 0 && total_rows > 0) return 0;
-  return nkv::meta_bytes(num_tokens) + 32 * capacity;
-}
-
-extern "C" int64_t nkv_store_gather_map_bytes(int64_t num_blocks) {
-  return num_blocks > 0 ? 8 * num_blocks : 0;
+  return nkv::meta_bytes(num_tokens) + 16 * capacity;
 }
 
 extern "C" int nkv_build_store_gather_plan(const int32_t* block_tables, int64_t table_stride,
@@ -370,62 +331,42 @@ extern "C" int nkv_build_store_gather_plan(const int32_t* block_tables, int64_t 
                                            const int32_t* cu_seqlens_k, int64_t num_seqs,
                                            int64_t num_tokens, int64_t out_rows,
                                            int64_t block_size, int64_t row_elems,
-                                           int64_t num_blocks, int32_t dtype, void* writer_map,
-                                           int64_t map_bytes, uint32_t step_tag, void* plan,
+                                           int64_t num_blocks, int32_t dtype, void* plan,
                                            int64_t plan_bytes, void* stream) {
   using namespace nkv;
   if (int rc = check_sg_geometry("nkv_build_store_gather_plan", num_tokens, num_seqs, out_rows,
                                  block_size, row_elems, num_blocks, dtype)) {
     return rc;
   }
-  if (table_stride < 0 || step_tag == 0) {
-    return nkv_fail(NKV_E_INVALID,
-                    "nkv_build_store_gather_plan: negative table_stride or zero step_tag");
+  if (table_stride < 0) {
+    return nkv_fail(NKV_E_INVALID, "nkv_build_store_gather_plan: negative table_stride");
   }
   const int64_t need = nkv_store_gather_plan_bytes(num_tokens, out_rows, num_seqs, block_size,
                                                    row_elems, dtype);
-  if (plan_bytes < need) {
-    return nkv_fail(NKV_E_CAPACITY, "nkv_build_store_gather_plan: plan of %lld bytes < %lld needed",
-                    static_cast<long long>(plan_bytes), static_cast<long long>(need));
-  }
-  if (map_bytes < nkv_store_gather_map_bytes(num_blocks)) {
-    return nkv_fail(NKV_E_CAPACITY, "nkv_build_store_gather_plan: writer map of %lld bytes < %lld",
-                    static_cast<long long>(map_bytes),
-                    static_cast<long long>(nkv_store_gather_map_bytes(num_blocks)));
-  }
+  if (int rc = check_plan_bytes("nkv_build_store_gather_plan", plan_bytes, need)) return rc;
   if (need == 0) return NKV_OK;
-  if (!plan || (num_blocks > 0 && !writer_map) ||
-      (num_seqs > 0 && (!cu_seqlens_q || !cu_seqlens_k)) ||
+  if (!plan || (num_seqs > 0 && (!cu_seqlens_q || !cu_seqlens_k)) ||
       (num_seqs > 0 && table_stride > 0 && !block_tables)) {
     return nkv_fail(NKV_E_INVALID, "nkv_build_store_gather_plan: null pointer");
   }
-  if (reinterpret_cast<uint64_t>(plan) % 16 != 0 || reinterpret_cast<uint64_t>(writer_map) % 8 != 0) {
-    return nkv_fail(NKV_E_INVALID,
-                    "nkv_build_store_gather_plan: plan must be 16-byte and map 8-byte aligned");
+  if (reinterpret_cast<uint64_t>(plan) % 16 != 0) {
+    return nkv_fail(NKV_E_INVALID, "nkv_build_store_gather_plan: plan must be 16-byte aligned");
   }
-  const int64_t capacity = (need - meta_bytes(num_tokens)) / 32;
+  const int64_t capacity = (need - meta_bytes(num_tokens)) / 16;
   const int64_t chunk_rows = nkv_gather_plan_rows(block_size, row_elems, dtype);
   auto* base = static_cast<uint8_t*>(plan);
-  auto* writers = static_cast<int64_t*>(writer_map);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (num_tokens > 0) {
-    int64_t blocks = (num_tokens + kSgMetaThreads - 1) / kSgMetaThreads;
-    if (blocks > 4096) blocks = 4096;
-    store_gather_meta_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kSgMetaThreads), 0, s>>>(
-        block_tables, table_stride, cu_seqlens_q, cu_seqlens_k, static_cast<int32_t>(num_seqs),
-        static_cast<int32_t>(num_tokens), static_cast<int32_t>(block_size), num_blocks, out_rows,
-        step_tag, writers, reinterpret_cast<int2*>(base));
-    if (int rc = nkv_check_launch("nkv_build_store_gather_plan")) return rc;
-  }
-  if (capacity == 0) return NKV_OK;
-  int64_t blocks = (capacity + kSgPlanThreads - 1) / kSgPlanThreads;
+  const int64_t items = capacity > num_tokens ? capacity : num_tokens;
+  int64_t blocks = (items + kSgPlanThreads - 1) / kSgPlanThreads;
+  if (blocks < 1) blocks = 1;
   if (blocks > 1024) blocks = 1024;
   const size_t lds = (static_cast<size_t>(num_seqs) + 1 + kSgPlanThreads / kWave + 1) *
                      sizeof(int32_t);
-  store_gather_chunk_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kSgPlanThreads), lds, s>>>(
+  store_gather_plan_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kSgPlanThreads), lds,
+                             static_cast<hipStream_t>(stream)>>>(
       block_tables, table_stride, cu_seqlens_q, cu_seqlens_k, static_cast<int32_t>(num_seqs),
-      static_cast<int32_t>(block_size), static_cast<int32_t>(chunk_rows), num_blocks, out_rows,
-      step_tag, writers, reinterpret_cast<int4*>(base + meta_bytes(num_tokens)), capacity);
+      static_cast<int32_t>(num_tokens), static_cast<int32_t>(block_size),
+      static_cast<int32_t>(chunk_rows), num_blocks, out_rows, reinterpret_cast<int2*>(base),
+      reinterpret_cast<int4*>(base + meta_bytes(num_tokens)), capacity);
   return nkv_check_launch("nkv_build_store_gather_plan");
 }
 
@@ -446,10 +387,7 @@ extern "C" int nkv_store_gather(const void* key, const void* value, void* key_ca
   }
   const int64_t need = nkv_store_gather_plan_bytes(num_tokens, out_rows, num_seqs, block_size,
                                                    row_elems, dtype);
-  if (plan_bytes < need) {
-    return nkv_fail(NKV_E_CAPACITY, "nkv_store_gather: plan of %lld bytes < %lld needed",
-                    static_cast<long long>(plan_bytes), static_cast<long long>(need));
-  }
+  if (int rc = check_plan_bytes("nkv_store_gather", plan_bytes, need)) return rc;
   if (num_tokens == 0 && out_rows == 0) return NKV_OK;
   if (!key_cache || !value_cache || !plan || (num_tokens > 0 && (!key || !value || !slot_mapping)) ||
       (out_rows > 0 && (!key_out || !value_out))) {
@@ -462,7 +400,7 @@ extern "C" int nkv_store_gather(const void* key, const void* value, void* key_ca
   const int64_t row_bytes = row_elems * eb;
   const int64_t ks = key_token_stride * eb;
   const int64_t vs = value_token_stride * eb;
-  const int64_t capacity = (need - meta_bytes(num_tokens)) / 32;
+  const int64_t capacity = (need - meta_bytes(num_tokens)) / 16;
   const int64_t chunk_rows = nkv_gather_plan_rows(block_size, row_elems, dtype);
   const int w = common_word_bytes(
       {reinterpret_cast<uint64_t>(key), reinterpret_cast<uint64_t>(value),

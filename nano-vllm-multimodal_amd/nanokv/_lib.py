@@ -65,11 +65,10 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         ),
     ),
     "nkv_store_gather_plan_bytes": (c_i64, (c_i64, c_i64, c_i64, c_i64, c_i64, c_i32)),
-    "nkv_store_gather_map_bytes": (c_i64, (c_i64,)),
     "nkv_build_store_gather_plan": (
         ctypes.c_int,
         (c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i32, c_ptr, c_i64,
-         ctypes.c_uint32, c_ptr, c_i64, c_ptr),
+         c_ptr),
     ),
     "nkv_store_gather": (
         ctypes.c_int,

@@ -195,25 +195,10 @@ class HIPPagedKVBackend:
         laid out for them."""
         self._load()
         num_blocks, block_size, heads, head_dim = cache.shape
-        writer_map, tag = self._writer_map(cache.device, num_blocks)
         return ops.build_store_gather_plan(
-            block_tables, cu_seqlens_q, cu_seqlens_k, writer_map, tag, num_tokens, total_tokens,
+            block_tables, cu_seqlens_q, cu_seqlens_k, num_tokens, total_tokens,
             num_blocks, block_size, heads * head_dim, cache.dtype,
         )
-
-    def _writer_map(self, device: torch.device, num_blocks: int) -> tuple[torch.Tensor, int]:
-        """The block -> writing request map of store_gather plans for caches
-        of ``num_blocks`` blocks on ``device`` (one int64 per block, zeroed
-        on creation), and the next step tag for it."""
-        key = (str(device), int(num_blocks))
-        with _LOAD_LOCK:
-            maps = self.__dict__.setdefault("_writer_maps", {})
-            entry = maps.get(key)
-            if entry is None or entry[1] >= 2**32 - 1:
-                entry = [torch.zeros(max(1, int(num_blocks)), dtype=torch.int64, device=device), 0]
-                maps[key] = entry
-            entry[1] += 1
-            return entry[0], entry[1]
 
     def store_gather(
         self,
@@ -234,11 +219,15 @@ class HIPPagedKVBackend:
         request's whole context (attention.py:87-93 then :250-259), in one
         launch: the caches end as :meth:`store` leaves them and the outputs
         equal :meth:`gather_varlen` over ``cu_seqlens_k`` afterwards.  Exact
-        when no slot repeats and each token's slot is -1 or the slot of its
-        own position in its request's block table, as prefill packing
-        produces.  ``plan`` from :meth:`build_store_gather_plan` (one per
-        step, built for these token and context counts) skips the planning
-        launch; ``out`` reuses output buffers."""
+        when no slot repeats, each token's slot is -1 or the slot of its own
+        position in its request's block table (as prefill packing produces,
+        model_runner.py:757-820), and no request's cached prefix holds a row
+        this call stores.  The reference's scheduler guarantees the last: a
+        block is hashed for prefix reuse only after the step that filled it
+        (scheduler.py:196-200, block_manager.py:229-258).  ``plan`` from
+        :meth:`build_store_gather_plan` (one per step, built for these token
+        and context counts) skips the planning launch; ``out`` reuses output
+        buffers."""
         validate_store_inputs(key, value, key_cache, value_cache, slot_mapping)
         validate_varlen_inputs(key_cache, value_cache, block_tables, cu_seqlens_k, total_tokens)
         if (cu_seqlens_q.dtype != torch.int32 or cu_seqlens_q.ndim != 1

@@ -27,10 +27,9 @@ too, paged_kv_cuda.cu:168-171).  Additive ops, with no reference schema:
                            Tensor first_part, float scale,
                            Tensor(a!) out) -> ()
     build_store_gather_plan(Tensor block_tables, Tensor cu_seqlens_q,
-                            Tensor cu_seqlens_k, Tensor(a!) writer_map,
-                            int step_tag, int num_tokens, int total_tokens,
-                            int num_blocks, int block_size, int row_elems,
-                            ScalarType dtype) -> Tensor
+                            Tensor cu_seqlens_k, int num_tokens,
+                            int total_tokens, int num_blocks, int block_size,
+                            int row_elems, ScalarType dtype) -> Tensor
     store_gather(Tensor key, Tensor value, Tensor(a!) key_cache,
                  Tensor(b!) value_cache, Tensor slot_mapping, Tensor plan,
                  int num_seqs, Tensor(c!) key_out, Tensor(d!) value_out) -> ()
@@ -65,9 +64,8 @@ SCHEMAS = {
     "Tensor value_cache, Tensor block_tables, Tensor plan, Tensor first_part, float scale, "
     "Tensor(a!) out) -> ()",
     "build_store_gather_plan": "build_store_gather_plan(Tensor block_tables, "
-    "Tensor cu_seqlens_q, Tensor cu_seqlens_k, Tensor(a!) writer_map, int step_tag, "
-    "int num_tokens, int total_tokens, int num_blocks, int block_size, int row_elems, "
-    "ScalarType dtype) -> Tensor",
+    "Tensor cu_seqlens_q, Tensor cu_seqlens_k, int num_tokens, int total_tokens, "
+    "int num_blocks, int block_size, int row_elems, ScalarType dtype) -> Tensor",
     "store_gather": "store_gather(Tensor key, Tensor value, Tensor(a!) key_cache, "
     "Tensor(b!) value_cache, Tensor slot_mapping, Tensor plan, int num_seqs, "
     "Tensor(c!) key_out, Tensor(d!) value_out) -> ()",
@@ -142,12 +140,28 @@ def _plan_capacity(total: int, num_seqs: int, block_size: int, row_elems: int, c
     )
 
 
+def _require_store_rows(key, value, key_cache, value_cache, slot_mapping) -> None:
+    """The sizes the store kernel trusts: the row size comes from the
+    caches, and one int32 slot is read per key row.  (The reference op
+    leaves these to the backend's validator; a direct op call that broke
+    them would address rows past the caches or the slot list.)"""
+    if (key.ndim != 3 or key.shape != value.shape or key_cache.ndim != 4
+            or key_cache.shape != value_cache.shape or key.shape[1:] != key_cache.shape[2:]):
+        raise RuntimeError("Paged KV HIP Store: key/value [tokens, kv_heads, head_dim] must match "
+                           "each other and the caches' [.., kv_heads, head_dim]")
+    if key.stride(-1) != 1 or value.stride(-1) != 1:
+        raise RuntimeError("Paged KV HIP Store: key/value inner dimensions must be contiguous")
+    if slot_mapping.ndim != 1 or slot_mapping.shape[0] != key.shape[0]:
+        raise RuntimeError("Paged KV HIP Store: slot_mapping must hold one slot per token")
+
+
 def _store_impl(key, value, key_cache, value_cache, slot_mapping) -> None:
     device = _require_device("paged KV HIP Store", key, value, key_cache, value_cache, slot_mapping)
     _require_contiguous_cache("paged KV HIP Store", key_cache, value_cache)
     if key.dtype != value.dtype or key.dtype != key_cache.dtype or key.dtype != value_cache.dtype:
         raise RuntimeError("Paged KV HIP Store dtype mismatch")
     slot_mapping = _int32_index("Paged KV HIP Store", "slot_mapping", slot_mapping)
+    _require_store_rows(key, value, key_cache, value_cache, slot_mapping)
     num_tokens = key.shape[0]
     if num_tokens == 0:
         return
@@ -281,30 +295,32 @@ def _gather_varlen_impl(key_cache, value_cache, block_tables, cu_seqlens_k, tota
     return key_out, value_out
 
 
+def _store_gather_plan_bytes(num_tokens: int, total_tokens: int, num_seqs: int, block_size: int,
+                             row_elems: int, code: int) -> int:
+    """Bytes of a store+gather plan for these counts (the int32 plan tensor
+    holds at least 16 bytes, exactly this many when it is non-zero)."""
+    return int(_lib.load_library().nkv_store_gather_plan_bytes(
+        num_tokens, total_tokens, num_seqs, block_size, row_elems, code))
+
+
 def _build_store_gather_plan_impl(
-    block_tables, cu_seqlens_q, cu_seqlens_k, writer_map, step_tag: int, num_tokens: int,
-    total_tokens: int, num_blocks: int, block_size: int, row_elems: int, dtype: torch.dtype,
+    block_tables, cu_seqlens_q, cu_seqlens_k, num_tokens: int, total_tokens: int,
+    num_blocks: int, block_size: int, row_elems: int, dtype: torch.dtype,
 ) -> torch.Tensor:
     device = _require_device("paged KV HIP store+gather plan", block_tables, cu_seqlens_q,
-                             cu_seqlens_k, writer_map)
-    if writer_map.dtype != torch.int64 or not writer_map.is_contiguous():
-        raise ValueError("writer_map must be a contiguous int64 tensor")
-    if not 0 < step_tag < 2**32:
-        raise ValueError("step_tag must be in [1, 2**32)")
+                             cu_seqlens_k)
     num_seqs = _require_cu("cu_seqlens_q", cu_seqlens_q)
     _require_cu("cu_seqlens_k", cu_seqlens_k, num_seqs)
     if block_tables.dtype != torch.int32 or block_tables.ndim != 2 or not block_tables.is_contiguous():
         raise ValueError("block_tables must be a contiguous two-dimensional int32 tensor")
     code = dtype_code(dtype)
-    library = _lib.load_library()
-    nbytes = int(library.nkv_store_gather_plan_bytes(num_tokens, total_tokens, num_seqs,
-                                                     block_size, row_elems, code))
+    nbytes = _store_gather_plan_bytes(num_tokens, total_tokens, num_seqs, block_size, row_elems,
+                                      code)
     plan = torch.empty(max(nbytes, 16) // 4, dtype=torch.int32, device=device)
-    status = library.nkv_build_store_gather_plan(
+    status = _lib.load_library().nkv_build_store_gather_plan(
         block_tables.data_ptr(), block_tables.shape[1], cu_seqlens_q.data_ptr(),
         cu_seqlens_k.data_ptr(), num_seqs, num_tokens, total_tokens, block_size, row_elems,
-        num_blocks, code, writer_map.data_ptr(), writer_map.numel() * 8, step_tag,
-        plan.data_ptr(), plan.numel() * 4, _stream(device),
+        num_blocks, code, plan.data_ptr(), nbytes, _stream(device),
     )
     _lib.check(status, "nanovllm_paged_kv::build_store_gather_plan")
     return plan
@@ -321,18 +337,29 @@ def _store_gather_impl(key, value, key_cache, value_cache, slot_mapping, plan, n
         raise ValueError("store+gather outputs must be contiguous")
     if key_out.shape != value_out.shape or key_out.shape[1:] != key_cache.shape[2:]:
         raise ValueError("store+gather outputs must be [rows, kv_heads, head_dim] of the caches")
+    slot_mapping = _int32_index("Paged KV HIP store+gather", "slot_mapping", slot_mapping)
+    _require_store_rows(key, value, key_cache, value_cache, slot_mapping)
     if plan.dtype != torch.int32 or plan.ndim != 1 or not plan.is_contiguous():
         raise ValueError("store+gather plan must be a contiguous 1-D int32 tensor")
+    if num_seqs < 0:
+        raise ValueError("num_seqs must be non-negative")
     if key.shape[1] > 1 and key.stride(1) != key.shape[2]:
         key = key.contiguous()
     if value.shape[1] > 1 and value.stride(1) != value.shape[2]:
         value = value.contiguous()
     num_blocks, block_size, heads, head_dim = key_cache.shape
+    code = dtype_code(key.dtype)
+    need = _store_gather_plan_bytes(key.shape[0], key_out.shape[0], num_seqs, block_size,
+                                    heads * head_dim, code)
+    if plan.numel() * 4 != max(need, 16):
+        raise ValueError(f"store+gather plan holds {plan.numel() * 4} bytes, {key.shape[0]} new "
+                         f"tokens and {key_out.shape[0]} context rows of {num_seqs} requests "
+                         f"need {max(need, 16)}: build it for the same counts")
     status = _lib.load_library().nkv_store_gather(
         key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
         slot_mapping.data_ptr(), key.shape[0], key.stride(0), value.stride(0), plan.data_ptr(),
-        plan.numel() * 4, num_seqs, key_out.shape[0], block_size, heads * head_dim, num_blocks,
-        dtype_code(key.dtype), key_out.data_ptr(), value_out.data_ptr(), _stream(device),
+        need, num_seqs, key_out.shape[0], block_size, heads * head_dim, num_blocks, code,
+        key_out.data_ptr(), value_out.data_ptr(), _stream(device),
     )
     _lib.check(status, "nanovllm_paged_kv::store_gather")
 

@@ -18,8 +18,8 @@ Cache contents are not generated here: callers fill caches on the device
   prefix_gather     32 contexts log-uniform [512, 32768], half sharing 8
                     prefix blocks, cache 8192 x 256
   narrow_rows       2x128 rows, 24 seqs of text + 1..3 image spans of 1296
-                    tokens, duplicated-image pairs share their prefix blocks,
-                    cache 16384 x 256
+                    tokens, duplicated-image pairs share their prefix blocks
+                    (filled and hashed in an earlier step), cache 16384 x 256
   decode_step       28 layers, 256 live contexts log-uniform [256, 16384],
                     16 evicted + 16 admitted, cache [2, 28, ~4.6k, 256, 8, 128]
 """
@@ -269,18 +269,37 @@ def prefix_gather(*, seed: int | None = None, num_seqs: int = 32, min_ctx: int =
     )
 
 
+NARROW_ROWS_SCHEDULES = ("reference", "same_step")
+
+
 def narrow_rows(*, seed: int | None = None, num_seqs: int = 24, num_blocks: int = 16384,
                 min_text: int = 16, max_text: int = 256, max_images: int = 3,
                 image_tokens: int = IMAGE_SPAN_TOKENS, heads: int = 2, head_dim: int = 128,
-                block_size: int = BLOCK_SIZE, dtype: torch.dtype = torch.bfloat16) -> Workload:
+                block_size: int = BLOCK_SIZE, dtype: torch.dtype = torch.bfloat16,
+                schedule: str = "reference") -> Workload:
     """Qwen2.5-VL-3B rows (2 x 128 bf16 = 512 B).  Each sequence is text
     segments (uniform in [min_text, max_text]) interleaved with 1..max_images
-    image spans.  Sequence 2k+1 duplicates sequence 2k's prefix up to and
-    including its first image; the full blocks of that prefix are shared
+    image spans.  Sequence 2k+1 duplicates sequence 2k's prompt up to and
+    including its first image, and reuses the full blocks of that prefix
     (prefix-cache reuse is by full blocks chained from block 0,
-    block_manager.py:120-198), so 2k+1 prefills only the rest.  The step is
-    a prefill store of every non-cached token followed by a gather of every
-    full context."""
+    block_manager.py:119-198).  The step is a prefill store of every
+    non-cached token followed by a gather of every full context.
+
+    ``schedule`` says when the shared blocks were filled:
+
+    * ``"reference"`` — in an earlier step, the only order the reference
+      produces: a block is hashed for reuse after the step that wrote it
+      (Scheduler.postprocess -> hash_blocks, scheduler.py:196-200,
+      block_manager.py:229-258).  Sequence 2k's first chunk prefilled its
+      first ``share`` full blocks, which were hashed; in this step 2k
+      continues from them and 2k+1 hits the same blocks, so both hold
+      share * block_size cached tokens and the step writes none of the
+      shared rows.
+    * ``"same_step"`` — 2k fills the blocks in this step and 2k+1 reads them
+      as its cached prefix.  The reference never schedules this; it is kept
+      as an extension for store-then-gather, which handles it."""
+    if schedule not in NARROW_ROWS_SCHEDULES:
+        raise ValueError(f"schedule must be one of {NARROW_ROWS_SCHEDULES}")
     g = _generator(seed_for("narrow_rows") if seed is None else seed)
     perm = torch.randperm(num_blocks, generator=g).numpy()
     cursor = 0
@@ -299,6 +318,11 @@ def narrow_rows(*, seed: int | None = None, num_seqs: int = 24, num_blocks: int 
             table = tables[-1][:share] + [int(b) for b in perm[cursor : cursor + n - share]]
             cursor += n - share
             cached.append(share * block_size)
+            if schedule == "reference":
+                # the partner's earlier chunk ended at the shared full blocks
+                # (it has text after its first image, so it still has new tokens)
+                assert share * block_size < totals[-1]
+                cached[-2] = share * block_size
         else:
             partner_first_text = int(texts[0])
             table = [int(b) for b in perm[cursor : cursor + n]]
@@ -317,7 +341,7 @@ def narrow_rows(*, seed: int | None = None, num_seqs: int = 24, num_blocks: int 
     return Workload(
         "narrow_rows", num_blocks, block_size, heads, head_dim, dtype, tables,
         totals.astype(np.int32), cached.astype(np.int32), scheduled.astype(np.int32),
-        totals.astype(np.int32), key, value, slots,
+        totals.astype(np.int32), key, value, slots, extra={"schedule": schedule},
     )
 
 

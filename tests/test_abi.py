@@ -55,11 +55,13 @@ def test_version_and_plan_geometry():
     assert lib.nkv_gather_plan_rows(256, 1024, 7) == 0
     assert lib.nkv_gather_plan_capacity(1000, 4, 256, 1024, 1) == -(-1000 // 16) + 4
     assert lib.nkv_gather_plan_capacity(0, 0, 256, 1024, 1) == 0
-    # store+gather plan: 8 bytes per token (rounded to 16) + 32 per chunk of cached rows
+    # store+gather plan: 8 bytes per token (rounded to 16) + 16 per chunk of cached rows
     cap = lib.nkv_gather_plan_capacity(1000, 4, 256, 1024, 1)
-    assert lib.nkv_store_gather_plan_bytes(5, 1000, 4, 256, 1024, 1) == 48 + 32 * cap
-    assert lib.nkv_store_gather_map_bytes(4096) == 8 * 4096
-    assert lib.nkv_store_gather_map_bytes(0) == 0
+    assert lib.nkv_store_gather_plan_bytes(5, 1000, 4, 256, 1024, 1) == 48 + 16 * cap
+    assert lib.nkv_store_gather_plan_bytes(0, 0, 0, 256, 1024, 1) == 0
+    # the plan of the rejection cases below: 8 tokens, 40 rows of 16 bytes in
+    # chunks of 16 rows, 2 requests -> 64 + 16 * (3 + 2)
+    assert lib.nkv_store_gather_plan_bytes(8, 40, 2, 16, 8, 1) == 144
 
 
 @pytest.mark.parametrize("call,message", [
@@ -80,21 +82,23 @@ def test_version_and_plan_geometry():
                                             256, 16, -0.5, 1, None, 0, None, 2048, None), "positive"),
     (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 8, 16, 128,
                                             256, 16, float("nan"), 1, None, 0, None, 2048, None), "finite"),
-    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 80, 0,
-                                             None, 4096, None), "step_tag"),
-    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 5000, 8, 40, 16, 8, 10, 1, None, 80, 1,
-                                             None, 4096, None), "num_seqs"),
-    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 80, 1,
-                                             None, 16, None), "plan of 16 bytes"),
-    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 40, 1,
-                                             None, 4096, None), "writer map"),
-    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 80, 1,
-                                             None, 4096, None), "null"),
+    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 5000, 8, 40, 16, 8, 10, 1, None, 144,
+                                             None), "num_seqs"),
+    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 16,
+                                             None), "plan of 16 bytes"),
+    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 4096,
+                                             None), "exactly 144"),
+    (lambda l: l.nkv_build_store_gather_plan(None, -4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 144,
+                                             None), "table_stride"),
+    (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 144,
+                                             None), "null"),
     (lambda l: l.nkv_store_gather(None, None, None, None, None, 8, 8, 8, None, 16, 2, 40, 16, 8, 10, 1,
                                   None, None, None), "plan of 16 bytes"),
-    (lambda l: l.nkv_store_gather(None, None, None, None, None, -1, 8, 8, None, 4096, 2, 40, 16, 8, 10, 1,
-                                  None, None, None), "out of range"),
     (lambda l: l.nkv_store_gather(None, None, None, None, None, 8, 8, 8, None, 4096, 2, 40, 16, 8, 10, 1,
+                                  None, None, None), "exactly 144"),
+    (lambda l: l.nkv_store_gather(None, None, None, None, None, -1, 8, 8, None, 144, 2, 40, 16, 8, 10, 1,
+                                  None, None, None), "out of range"),
+    (lambda l: l.nkv_store_gather(None, None, None, None, None, 8, 8, 8, None, 144, 2, 40, 16, 8, 10, 1,
                                   None, None, None), "null"),
     (lambda l: l.nkv_pack_decode(None, None, None, 0, 5000, 5000, 16, 4, 4, None, None, None, None, None), "num_seqs"),
     (lambda l: l.nkv_pack_decode(None, None, None, 0, 3, 3, 16, 4, 4, None, None, None, None, None), "null"),

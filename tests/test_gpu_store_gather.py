@@ -2,11 +2,12 @@
 oracle's store followed by its varlen gather, bit-exact.
 
 Covers the chunked-prefill and narrow-row workloads at full size (the
-narrow-row step has requests whose cached prefix is in blocks another
-request of the same step is filling), random prefill batches with shared
-blocks, continuation chunks, empty requests and -1 slots, plans shared by
-two layers, and a later step that must not see the previous step's
-writers."""
+narrow-row step in the reference's order: duplicated-image requests hit
+prefix blocks filled and hashed in an earlier step), random prefill batches
+whose requests share earlier-step prefix blocks, continuation chunks, empty
+requests and -1 slots, plans shared by two layers, two consecutive steps,
+the decode shape, the plan's layout, and plans or inputs the op must
+reject before any launch."""
 from __future__ import annotations
 
 import numpy as np
@@ -92,20 +93,23 @@ def test_workload_full_size(backend, gpu_device, name):
                    wl.padded_block_tables(), wl.slot_mapping, cu_q, wl.cu_seqlens_k())
 
 
-def _prefill_batch(rng, num_seqs, bs, nb, *, share_in_step=True, minus_one=0, empty=True):
+def _prefill_batch(rng, num_seqs, bs, nb, *, share=True, minus_one=0, empty=True):
     """Requests with cached prefixes and new tokens, block lists from a
-    permutation; with ``share_in_step`` odd requests take their first blocks
-    from the previous request's blocks, which that request fills in this
-    step (its cached prefix is then written in the same step)."""
+    permutation.  With ``share``, an odd request whose predecessor holds full
+    cached blocks reuses some of them as its own cached prefix: blocks the
+    predecessor filled in an earlier step, hashed after that step, as the
+    reference's prefix cache hands them out (scheduler.py:196-200,
+    block_manager.py:119-198,229-258), so no new row of the batch lands in
+    any request's cached prefix."""
     perm = list(rng.permutation(nb))
     tables, cached, scheduled = [], [], []
     for i in range(num_seqs):
-        if share_in_step and i % 2 == 1 and scheduled[-1] > bs and cached[-1] == 0:
-            share = int(rng.integers(1, scheduled[-1] // bs + 1))
-            c = share * bs
+        if share and i % 2 == 1 and cached[-1] >= bs:
+            hit = int(rng.integers(1, cached[-1] // bs + 1))
+            c = hit * bs
             q = int(rng.integers(0 if empty else 1, 3 * bs))
-            need = -(-(c + q) // bs)
-            t = tables[-1][:share] + [perm.pop() for _ in range(need - share)]
+            need = max(hit, -(-(c + q) // bs))
+            t = tables[-1][:hit] + [perm.pop() for _ in range(need - hit)]
         else:
             c = int(rng.integers(0, 3)) * bs + (int(rng.integers(0, bs)) if rng.random() < 0.3 else 0)
             q = int(rng.integers(0 if empty else 1, 4 * bs))
@@ -130,6 +134,17 @@ def _prefill_batch(rng, num_seqs, bs, nb, *, share_in_step=True, minus_one=0, em
     return table, slots, cu_q, cu_k
 
 
+def _cached_rows_untouched(table, slots, cu_q, cu_k, bs) -> bool:
+    """No request's cached prefix holds a slot that the batch stores."""
+    written = set(slots[slots >= 0].tolist())
+    for i in range(len(cu_q) - 1):
+        cached = int(cu_k[i + 1] - cu_k[i]) - int(cu_q[i + 1] - cu_q[i])
+        for p in range(cached):
+            if int(table[i, p // bs]) * bs + p % bs in written:
+                return False
+    return True
+
+
 @pytest.mark.parametrize("dtype,heads,dim,bs,seed", [
     (torch.bfloat16, 8, 128, 256, 1),
     (torch.bfloat16, 2, 128, 256, 2),
@@ -142,6 +157,7 @@ def test_random_prefill_batches(backend, gpu_device, dtype, heads, dim, bs, seed
     rng = np.random.default_rng(seed * 100 + minus_one)
     nb = 4000
     table, slots, cu_q, cu_k = _prefill_batch(rng, 23, bs, nb, minus_one=minus_one)
+    assert _cached_rows_untouched(table, slots, cu_q, cu_k, bs)
     g = torch.Generator(device=gpu_device).manual_seed(seed)
     kc = torch.randn(nb, bs, heads, dim, device=gpu_device, generator=g).to(dtype)
     vc = torch.randn(nb, bs, heads, dim, device=gpu_device, generator=g).to(dtype)
@@ -175,10 +191,10 @@ def test_fused_qkv_views_and_one_plan_for_two_layers(backend, gpu_device):
                        table, slots, cu_q, cu_k, plan=plan)
 
 
-def test_next_step_ignores_previous_writers(backend, gpu_device):
-    """Step A writes blocks that its other requests read as cached prefix;
-    step B reads those blocks as plain cached rows (nobody writes them in
-    B), so B must take them from the cache, not from A's tokens."""
+def test_two_consecutive_steps(backend, gpu_device):
+    """Step A stores its requests' new rows; in step B the same requests
+    continue with one new token each, and every row A stored is now part of
+    a cached prefix that B's launch copies from the cache."""
     rng = np.random.default_rng(5)
     bs, heads, dim, nb = 16, 2, 64, 800
     g = torch.Generator(device=gpu_device).manual_seed(5)
@@ -232,10 +248,9 @@ def test_empty_step_and_context_only(backend, gpu_device):
 
 def _expected_plan(tables, cu_q, cu_k, bs, chunk, num_blocks):
     """The plan restated on the host: per token {output row, slot of its
-    position}; per cached chunk {source row, output row, rows, request} and
-    {token of the chunk's first row, [lo, hi) rows written in this step}."""
+    position}; per cached chunk {source row, output row, rows, request}."""
     num_seqs = len(cu_q) - 1
-    meta, writer = [], {}
+    meta = []
     for t in range(int(cu_q[-1])):
         i = int(np.searchsorted(cu_q, t, side="right")) - 1
         lk, lq = int(cu_k[i + 1] - cu_k[i]), int(cu_q[i + 1] - cu_q[i])
@@ -243,8 +258,6 @@ def _expected_plan(tables, cu_q, cu_k, bs, chunk, num_blocks):
         block = int(tables[i, p // bs]) if p // bs < tables.shape[1] else -1
         slot = block * bs + p % bs if 0 <= block < num_blocks else -1
         meta.append((int(cu_k[i]) + p, slot))
-        if slot >= 0 and (p % bs == 0 or t == cu_q[i]):
-            writer[block] = (i, p // bs)
     entries = []
     for i in range(num_seqs):
         cached = int(cu_k[i + 1] - cu_k[i]) - int(cu_q[i + 1] - cu_q[i])
@@ -252,25 +265,14 @@ def _expected_plan(tables, cu_q, cu_k, bs, chunk, num_blocks):
             rows = min(chunk, cached - row0)
             block = int(tables[i, row0 // bs]) if row0 // bs < tables.shape[1] else -1
             src = block * bs + row0 % bs if 0 <= block < num_blocks else -1
-            tail = (0, 0, 0, 0)
-            if src >= 0 and block in writer:
-                w, wl = writer[block]
-                wlk = int(cu_k[w + 1] - cu_k[w])
-                wstart = wlk - int(cu_q[w + 1] - cu_q[w])
-                first = wl * bs + row0 % bs
-                lo = max(0, min(rows, wstart - first))
-                hi = max(lo, min(rows, wlk - first))
-                if lo < hi:
-                    tail = (int(cu_q[w]) + first - wstart, lo, hi, 0)
-            entries.append((src, int(cu_k[i]) + row0, rows, i) + tail)
+            entries.append((src, int(cu_k[i]) + row0, rows, i))
     return meta, entries
 
 
 @pytest.mark.parametrize("source", ["narrow_rows", "random"])
-def test_plan_marks_rows_written_in_the_step(backend, gpu_device, source):
-    """The plan, read back, equals its host restatement: every cached chunk
-    whose rows another request writes in this step names that token range
-    (the fused launch takes those rows from K/V, never from the cache)."""
+def test_plan_matches_host_restatement(backend, gpu_device, source):
+    """The plan, read back, equals its host restatement: every token's
+    output row and slot, every cached-prefix chunk, zeros past the last."""
     from nanokv import _lib, workloads
 
     if source == "narrow_rows":
@@ -290,14 +292,61 @@ def test_plan_marks_rows_written_in_the_step(backend, gpu_device, source):
     meta, entries = _expected_plan(tables, cu_q, cu_k, bs, chunk, nb)
     meta_words = (t * 8 + 15) // 16 * 4
     np.testing.assert_array_equal(plan[:2 * t].reshape(t, 2), np.asarray(meta, np.int32).reshape(t, 2))
-    got = plan[meta_words:].reshape(-1, 8)
-    assert len(entries) <= got.shape[0]
-    np.testing.assert_array_equal(got[:len(entries)], np.asarray(entries, np.int32).reshape(-1, 8))
+    got = plan[meta_words:].reshape(-1, 4)
+    assert 0 < len(entries) <= got.shape[0]
+    np.testing.assert_array_equal(got[:len(entries)], np.asarray(entries, np.int32).reshape(-1, 4))
     assert (got[len(entries):] == 0).all()
-    written = sum(1 for e in entries if e[6] > e[5])
-    print(f"[store_gather plan {source}] {len(entries)} cached chunks, {written} with rows written "
-          f"in the step", flush=True)
-    assert written > 0
+    print(f"[store_gather plan {source}] {t} tokens, {len(entries)} cached chunks", flush=True)
+
+
+def test_plan_and_inputs_rejected_before_launch(backend, gpu_device):
+    """A plan built for other token or context counts, an int64 or short
+    slot_mapping, and a key narrower than the cache's rows all raise on the
+    host; the caches and outputs stay as they were."""
+    from nanokv.paged_kv import ops
+
+    rng = np.random.default_rng(12)
+    bs, heads, dim, nb = 16, 2, 64, 300
+    table, slots, cu_q, cu_k = _prefill_batch(rng, 6, bs, nb, empty=False)
+    t, total = int(cu_q[-1]), int(cu_k[-1])
+    g = torch.Generator(device=gpu_device).manual_seed(12)
+    kc = torch.randn(nb, bs, heads, dim, device=gpu_device, generator=g).to(torch.bfloat16)
+    vc = torch.randn_like(kc)
+    before_k, before_v = kc.clone(), vc.clone()
+    key = torch.randn(t, heads, dim, device=gpu_device, generator=g).to(torch.bfloat16)
+    value = torch.randn_like(key)
+    d_tables = torch.from_numpy(table).to(gpu_device)
+    d_cu_q, d_cu_k = torch.from_numpy(cu_q).to(gpu_device), torch.from_numpy(cu_k).to(gpu_device)
+    d_slots = torch.from_numpy(slots).to(gpu_device)
+    k_out = torch.zeros(total, heads, dim, device=gpu_device, dtype=torch.bfloat16)
+    v_out = torch.zeros_like(k_out)
+    n = len(cu_q) - 1
+    good = backend.build_store_gather_plan(kc, d_tables, d_cu_q, d_cu_k, t, total)
+    # (8 bytes of plan per token, in 16-byte steps: two more tokens move the chunk entries)
+    wrong = [backend.build_store_gather_plan(kc, d_tables, d_cu_q, d_cu_k, t + 2, total),
+             backend.build_store_gather_plan(kc, d_tables, d_cu_q, d_cu_k, t, total + 4 * 1024)]
+    for plan in wrong:
+        with pytest.raises(ValueError, match="plan"):
+            backend.store_gather(key, value, kc, vc, d_slots, d_tables, d_cu_q, d_cu_k, total,
+                                 plan=plan, out=(k_out, v_out))
+        with pytest.raises(ValueError, match="plan"):
+            ops.store_gather(key, value, kc, vc, d_slots, plan, n, k_out, v_out)
+    bad_inputs = [
+        (key, value, d_slots.long(), "int32"),                   # int64 slots
+        (key, value, d_slots[:-1], "one slot per token"),        # short slot_mapping
+        (key[:, :1], value[:, :1], d_slots, "must match"),       # fewer kv heads than the cache
+    ]
+    for k, v, sl, message in bad_inputs:
+        with pytest.raises(RuntimeError, match=message):
+            ops.store_gather(k, v, kc, vc, sl, good, n, k_out, v_out)
+        with pytest.raises(RuntimeError, match=message):
+            torch.ops.nanovllm_paged_kv.store_gather(k, v, kc, vc, sl, good, n, k_out, v_out)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(torch.int16), before_k.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), before_v.view(torch.int16))
+    assert not k_out.view(torch.int16).any() and not v_out.view(torch.int16).any()
+    # the good plan still runs, and the op matches the oracle
+    _run_and_check(backend, gpu_device, kc, vc, key, value, table, slots, cu_q, cu_k, plan=good)
 
 
 def test_decode_step_shape(backend, gpu_device):
