@@ -51,6 +51,20 @@ extern "C" {
 /* Library version (major*10000 + minor*100 + patch). */
 int nkv_version(void);
 
+/*
+ * Build id: "<sources>-<config>", where <sources> is 16 hex digits of a
+ * SHA-256 over every source and header file, the compiler flags and the
+ * offload architecture, and <config> is "default" or 8 hex digits of the
+ * launch-shape defines the library was compiled with.  A loader recomputes
+ * <sources> from the files on disk and refuses a library that differs.
+ *
+ * Replaces: the reference's build fingerprint, which names the extension
+ *   build after a SHA-256 of its sources, flags, toolchain and arch list so
+ *   that a changed source rebuilds it (nanovllm/layers/paged_kv/
+ *   loader.py:47-85, tested in tests/test_paged_kv_extension_loader.py:12-32).
+ */
+const char* nkv_build_id(void);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* nkv_last_error(void);
 

@@ -32,6 +32,15 @@ int nkv_check_launch(const char* what) {
 
 extern "C" int nkv_version(void) { return 100; }
 
+// Fingerprint of the sources, headers, compiler flags and target this
+// library was compiled from, passed in by the build recipe
+// (nanokv/build.py); the loader recomputes it from the sources on disk and
+// refuses a library built from other ones.
+#ifndef NKV_BUILD_ID
+#define NKV_BUILD_ID "unfingerprinted"
+#endif
+extern "C" const char* nkv_build_id(void) { return NKV_BUILD_ID; }
+
 extern "C" const char* nkv_last_error(void) { return g_last_error.c_str(); }
 
 namespace nkv {

@@ -4,6 +4,15 @@ The library is loaded lazily, once, under a lock (the double-checked load of
 the reference's CUDA backend, nanovllm/layers/paged_kv/cuda_backend.py:21-42).
 A missing or unloadable library raises ``RuntimeError`` with the path and the
 loader's message: there is no fallback path.
+
+A library built from other sources than the ones on disk is refused: the
+build bakes a fingerprint of its sources, headers, flags and target into
+``nkv_build_id()``, and loading recomputes it from the files (the reference
+names its extension build after such a fingerprint and rebuilds when it
+changes, nanovllm/layers/paged_kv/loader.py:47-112).  The in-tree library
+must match exactly, launch-shape defines included; a ``$NANOKV_LIBRARY``
+override (a build with other defines) must match the sources, and its full
+id is reported by :func:`build_id`.
 """
 from __future__ import annotations
 
@@ -12,6 +21,7 @@ import os
 from pathlib import Path
 from threading import Lock
 
+from nanokv import build as _build
 from nanokv.build import LIBRARY_PATH
 
 c_i32 = ctypes.c_int32
@@ -38,6 +48,7 @@ c_pool = ctypes.POINTER(PoolDesc)
 # name -> (restype, argtypes); mirrors include/nanokv.h.
 SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     "nkv_version": (ctypes.c_int, ()),
+    "nkv_build_id": (ctypes.c_char_p, ()),
     "nkv_last_error": (ctypes.c_char_p, ()),
     "nkv_store": (
         ctypes.c_int,
@@ -170,6 +181,50 @@ def library_path() -> str:
     return os.environ.get("NANOKV_LIBRARY") or str(LIBRARY_PATH)
 
 
+def verify_build_id(found: str, path: Path, *, override: bool, source_dir: Path = _build.SOURCE_DIR,
+                    include_dir: Path = _build.INCLUDE_DIR) -> None:
+    """Raise RuntimeError when the library at ``path`` (whose nkv_build_id()
+    is ``found``) was not built from the sources in ``source_dir`` and
+    ``include_dir``.  Without the sources (an install that ships only the
+    library) there is nothing to compare against."""
+    if not all(f.is_file() for f in _build.fingerprint_files(Path(source_dir), Path(include_dir))):
+        return
+    sources = _build.source_fingerprint(source_dir, include_dir)
+    expected = f"{sources}-{_build.config_tag(None)}"
+    stale = not found.startswith(sources + "-") if override else found != expected
+    if stale:
+        raise RuntimeError(
+            f"{path} is stale: built as {found!r}, the sources in {source_dir} give "
+            f"{expected!r}{' (any launch-shape config)' if override else ''}; rebuild it "
+            "(__graft_entry__.build() or python -m nanokv.build)")
+
+
+def open_library(path: Path, *, override: bool = False, source_dir: Path = _build.SOURCE_DIR,
+                 include_dir: Path = _build.INCLUDE_DIR) -> ctypes.CDLL:
+    """Load the library at ``path``, check its build id against the sources
+    and bind every entry point of the ABI."""
+    path = Path(path)
+    if not path.is_file():
+        raise RuntimeError(
+            f"nanokv HIP library not built: {path} is missing "
+            "(run __graft_entry__.build() or python -m nanokv.build)"
+        )
+    try:
+        library = ctypes.CDLL(str(path))
+    except OSError as exc:
+        raise RuntimeError(f"failed to load {path}: {exc}") from exc
+    for name, (restype, argtypes) in SIGNATURES.items():
+        try:
+            function = getattr(library, name)
+        except AttributeError as exc:
+            raise RuntimeError(f"{path} does not export {name}") from exc
+        function.restype = restype
+        function.argtypes = list(argtypes)
+    found = library.nkv_build_id().decode("utf-8", "replace")
+    verify_build_id(found, path, override=override, source_dir=source_dir, include_dir=include_dir)
+    return library
+
+
 def load_library() -> ctypes.CDLL:
     """Return the loaded library, loading it on first use."""
     global _LIBRARY
@@ -177,25 +232,15 @@ def load_library() -> ctypes.CDLL:
         return _LIBRARY
     with _LOCK:
         if _LIBRARY is None:
-            path = Path(library_path())
-            if not path.is_file():
-                raise RuntimeError(
-                    f"nanokv HIP library not built: {path} is missing "
-                    "(run __graft_entry__.build() or python -m nanokv.build)"
-                )
-            try:
-                library = ctypes.CDLL(str(path))
-            except OSError as exc:
-                raise RuntimeError(f"failed to load {path}: {exc}") from exc
-            for name, (restype, argtypes) in SIGNATURES.items():
-                try:
-                    function = getattr(library, name)
-                except AttributeError as exc:
-                    raise RuntimeError(f"{path} does not export {name}") from exc
-                function.restype = restype
-                function.argtypes = list(argtypes)
-            _LIBRARY = library
+            _LIBRARY = open_library(Path(library_path()),
+                                    override=bool(os.environ.get("NANOKV_LIBRARY")))
     return _LIBRARY
+
+
+def build_id() -> str:
+    """nkv_build_id() of the loaded library: the fingerprint of the sources
+    it was built from and its launch-shape config."""
+    return load_library().nkv_build_id().decode("utf-8", "replace")
 
 
 def check(status: int, what: str) -> None:

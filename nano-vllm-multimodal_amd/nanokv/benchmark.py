@@ -172,6 +172,13 @@ def environment_identity(device=None) -> dict:
         "cpu_count": os.cpu_count(),
         "host_threads": host_threads(),
     }
+    try:
+        from nanokv import _lib
+
+        identity["nanokv_build_id"] = _lib.build_id()
+        identity["nanokv_library"] = _lib.library_path()
+    except RuntimeError as exc:  # not built: the identity says so
+        identity["nanokv_build_id"] = f"unavailable: {exc}"
     if device is not None and torch.cuda.is_available():
         props = torch.cuda.get_device_properties(device)
         identity.update({

@@ -7,6 +7,7 @@ Run ``python -m nanokv.build`` (with ``nano-vllm-multimodal_amd`` on
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -46,6 +47,46 @@ HIPCC_FLAGS = (
 )
 
 
+# Headers the sources include: part of the fingerprint with the sources.
+HEADERS = ("nkv_common.h", "nkv_mfma.h")
+
+
+def fingerprint_files(source_dir: Path = SOURCE_DIR, include_dir: Path = INCLUDE_DIR) -> list[Path]:
+    return ([source_dir / name for name in SOURCES] + [source_dir / name for name in HEADERS]
+            + [include_dir / "nanokv.h"])
+
+
+def source_fingerprint(source_dir: Path = SOURCE_DIR, include_dir: Path = INCLUDE_DIR) -> str:
+    """16 hex digits of a SHA-256 over every source and header (name and
+    bytes), the compiler flags and the offload architecture, each field
+    length-prefixed so that no two inputs collide by concatenation.  The
+    reference names its extension build after the same kind of digest
+    (nanovllm/layers/paged_kv/loader.py:47-85)."""
+    digest = hashlib.sha256()
+    fields: list[bytes] = []
+    for path in fingerprint_files(Path(source_dir), Path(include_dir)):
+        fields += [path.name.encode(), path.read_bytes()]
+    fields += ["\0".join(HIPCC_FLAGS).encode(), OFFLOAD_ARCH.encode()]
+    for field in fields:
+        digest.update(len(field).to_bytes(8, "little"))
+        digest.update(field)
+    return digest.hexdigest()[:16]
+
+
+def config_tag(defines: dict[str, object] | None = None) -> str:
+    """"default", or 8 hex digits of the launch-shape defines."""
+    if not defines:
+        return "default"
+    text = "\0".join(f"{key}={value}" for key, value in sorted(defines.items()))
+    return hashlib.sha256(text.encode()).hexdigest()[:8]
+
+
+def build_id(defines: dict[str, object] | None = None, source_dir: Path = SOURCE_DIR,
+             include_dir: Path = INCLUDE_DIR) -> str:
+    """The id nkv_build_id() of a library built from these files returns."""
+    return f"{source_fingerprint(source_dir, include_dir)}-{config_tag(defines)}"
+
+
 def hipcc_path() -> str:
     candidates = []
     rocm = os.environ.get("ROCM_PATH") or os.environ.get("HIP_PATH")
@@ -61,32 +102,39 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (set ROCM_PATH); cannot build libnanokv.so")
 
 
-def build_command(output: Path, defines: dict[str, object] | None = None) -> list[str]:
+def build_command(output: Path, defines: dict[str, object] | None = None,
+                  source_dir: Path = SOURCE_DIR, include_dir: Path = INCLUDE_DIR) -> list[str]:
+    identity = build_id(defines, source_dir, include_dir)
     return [
         hipcc_path(),
         *HIPCC_FLAGS,
         *(f"-D{key}={value}" for key, value in (defines or {}).items()),
-        f"-I{INCLUDE_DIR}",
-        *(str(SOURCE_DIR / name) for name in SOURCES),
+        f'-DNKV_BUILD_ID="{identity}"',
+        f"-I{include_dir}",
+        *(str(Path(source_dir) / name) for name in SOURCES),
         "-o",
         str(output),
     ]
 
 
 def build(*, verbose: bool = False, output: Path | None = None,
-          defines: dict[str, object] | None = None) -> Path:
+          defines: dict[str, object] | None = None, source_dir: Path | None = None,
+          include_dir: Path | None = None) -> Path:
     """Compile the library (always, even if a build exists) and install it
     atomically at ``output`` (default :data:`LIBRARY_PATH`).  ``defines``
     override the kernels' compile-time launch-shape knobs
     (NKV_GATHER_THREADS, NKV_GATHER_UNROLL, NKV_GATHER_NT_LOADS,
-    NKV_GATHER_NT_STORES, NKV_GATHER_CHUNK_BYTES)."""
+    NKV_GATHER_NT_STORES, NKV_GATHER_CHUNK_BYTES).  The library reports
+    :func:`build_id` of its sources and defines through nkv_build_id()."""
     target = Path(output) if output is not None else LIBRARY_PATH
-    missing = [name for name in SOURCES if not (SOURCE_DIR / name).is_file()]
+    source_dir = Path(source_dir) if source_dir is not None else SOURCE_DIR
+    include_dir = Path(include_dir) if include_dir is not None else INCLUDE_DIR
+    missing = [str(path) for path in fingerprint_files(source_dir, include_dir) if not path.is_file()]
     if missing:
         raise RuntimeError(f"nanokv sources missing: {', '.join(missing)}")
     with tempfile.TemporaryDirectory(prefix="nanokv-build-") as tmp:
         output = Path(tmp) / LIBRARY_PATH.name
-        command = build_command(output, defines)
+        command = build_command(output, defines, source_dir, include_dir)
         if verbose:
             print(" ".join(command), flush=True)
         result = subprocess.run(command, capture_output=True, text=True)
