@@ -87,6 +87,55 @@ def index_value_validation_enabled(tensor: torch.Tensor) -> bool:
     return flag in ("1", "true", "yes", "on")
 
 
+def _same_device(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """``a.device == b.device`` without building device objects: GPU tensors
+    compare by index; host-side ones (index -1) fall back to the devices."""
+    index = a.get_device()
+    if index != b.get_device():
+        return False
+    return index >= 0 or a.device == b.device
+
+
+def check_store_inputs(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """The checks of base.py:75-114, in its order and with its messages,
+    without building the StoreDimensions record (the per-call path of the
+    hip backend; :func:`validate_store_inputs` wraps it)."""
+    kshape = key.shape
+    if key.ndim != 3 or value.ndim != 3 or kshape != value.shape:
+        raise ValueError("key and value must have matching shape [tokens, kv_heads, head_dim]")
+    if key.stride(-1) != 1 or value.stride(-1) != 1:
+        raise ValueError("key and value inner dimensions must be contiguous")
+    cshape = key_cache.shape
+    if key_cache.ndim != 4 or value_cache.ndim != 4 or cshape != value_cache.shape:
+        raise ValueError("key and value cache shape must match [blocks, block, kv_heads, head_dim]")
+    if cshape[2] != kshape[1] or cshape[3] != kshape[2]:
+        raise ValueError("cache shape does not match key/value kv_heads and head_dim")
+    if not (_same_device(key, value) and _same_device(key, key_cache)
+            and _same_device(key, value_cache) and _same_device(key, slot_mapping)):
+        raise ValueError("all paged KV Store tensors must be on the same device")
+    dtype = key.dtype
+    if not (dtype == value.dtype == key_cache.dtype == value_cache.dtype):
+        raise ValueError("key, value, and caches must have matching dtype")
+    if slot_mapping.dtype != torch.int32 or slot_mapping.ndim != 1:
+        raise ValueError("slot_mapping must be a one-dimensional int32 tensor")
+    num_tokens = kshape[0]
+    if slot_mapping.shape[0] != num_tokens:
+        raise ValueError("slot_mapping length must equal the number of input tokens")
+    if not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be contiguous")
+    if num_tokens and index_value_validation_enabled(slot_mapping):
+        num_slots = cshape[0] * cshape[1]
+        out_of_range = (slot_mapping < -1) | (slot_mapping >= num_slots)
+        if bool(out_of_range.any()):
+            raise ValueError(f"slot_mapping contains a slot outside [-1, {num_slots})")
+
+
 def validate_store_inputs(
     key: torch.Tensor,
     value: torch.Tensor,
@@ -95,59 +144,47 @@ def validate_store_inputs(
     slot_mapping: torch.Tensor,
 ) -> StoreDimensions:
     """base.py:75-114."""
-    if key.ndim != 3 or value.ndim != 3 or key.shape != value.shape:
-        raise ValueError("key and value must have matching shape [tokens, kv_heads, head_dim]")
-    if key.stride(-1) != 1 or value.stride(-1) != 1:
-        raise ValueError("key and value inner dimensions must be contiguous")
-    if key_cache.ndim != 4 or value_cache.ndim != 4 or key_cache.shape != value_cache.shape:
-        raise ValueError("key and value cache shape must match [blocks, block, kv_heads, head_dim]")
+    check_store_inputs(key, value, key_cache, value_cache, slot_mapping)
     num_tokens, num_kv_heads, head_dim = key.shape
-    num_blocks, block_size, cache_heads, cache_dim = key_cache.shape
-    if cache_heads != num_kv_heads or cache_dim != head_dim:
-        raise ValueError("cache shape does not match key/value kv_heads and head_dim")
-    devices = {t.device for t in (key, value, key_cache, value_cache, slot_mapping)}
-    if len(devices) != 1:
-        raise ValueError("all paged KV Store tensors must be on the same device")
-    if not (key.dtype == value.dtype == key_cache.dtype == value_cache.dtype):
-        raise ValueError("key, value, and caches must have matching dtype")
-    if slot_mapping.dtype != torch.int32 or slot_mapping.ndim != 1:
-        raise ValueError("slot_mapping must be a one-dimensional int32 tensor")
-    if slot_mapping.numel() != num_tokens:
-        raise ValueError("slot_mapping length must equal the number of input tokens")
-    if not slot_mapping.is_contiguous():
-        raise ValueError("slot_mapping must be contiguous")
-    num_slots = num_blocks * block_size
-    if slot_mapping.numel() and index_value_validation_enabled(slot_mapping):
-        out_of_range = (slot_mapping < -1) | (slot_mapping >= num_slots)
-        if bool(out_of_range.any()):
-            raise ValueError(f"slot_mapping contains a slot outside [-1, {num_slots})")
+    num_blocks, block_size = key_cache.shape[:2]
     return StoreDimensions(num_tokens, num_blocks, block_size, num_kv_heads, head_dim)
 
 
-def validate_gather_inputs(
-    cache: torch.Tensor, block_table: torch.Tensor, sequence_length: int
-) -> GatherDimensions:
-    """base.py:117-151."""
+def check_gather_inputs(cache: torch.Tensor, block_table: torch.Tensor, sequence_length: int) -> int:
+    """The checks of base.py:117-151, in its order and with its messages;
+    returns the required block count without building the GatherDimensions
+    record (the per-call path of the hip backend; :func:`validate_gather_inputs`
+    wraps it).  The table prefix is sliced only when index values are
+    checked."""
     if cache.ndim != 4:
         raise ValueError("cache must have shape [blocks, block, kv_heads, head_dim]")
     if cache.stride(-1) != 1:
         raise ValueError("cache inner dimensions must be contiguous")
     if block_table.dtype != torch.int32 or block_table.ndim != 1:
         raise ValueError("block_table must be a one-dimensional int32 tensor")
-    if block_table.device != cache.device:
+    if not _same_device(block_table, cache):
         raise ValueError("cache and block_table must be on the same device")
     if not block_table.is_contiguous():
         raise ValueError("block_table must be contiguous")
     if sequence_length < 0:
         raise ValueError("sequence_length must be non-negative")
-    num_blocks, block_size, num_kv_heads, head_dim = cache.shape
+    block_size = cache.shape[1]
     required_blocks = -(-sequence_length // block_size)
-    if block_table.numel() < required_blocks:
+    if block_table.shape[0] < required_blocks:
         raise ValueError("block_table does not cover the requested sequence length")
-    used = block_table[:required_blocks]
-    if used.numel() and index_value_validation_enabled(used):
-        if bool(((used < 0) | (used >= num_blocks)).any()):
+    if required_blocks and index_value_validation_enabled(block_table):
+        used = block_table[:required_blocks]
+        if bool(((used < 0) | (used >= cache.shape[0])).any()):
             raise ValueError("block_table contains an invalid physical block")
+    return required_blocks
+
+
+def validate_gather_inputs(
+    cache: torch.Tensor, block_table: torch.Tensor, sequence_length: int
+) -> GatherDimensions:
+    """base.py:117-151."""
+    required_blocks = check_gather_inputs(cache, block_table, sequence_length)
+    _, block_size, num_kv_heads, head_dim = cache.shape
     return GatherDimensions(sequence_length, required_blocks, block_size, num_kv_heads, head_dim)
 
 

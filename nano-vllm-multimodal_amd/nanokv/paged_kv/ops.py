@@ -155,64 +155,94 @@ def _require_store_rows(key, value, key_cache, value_cache, slot_mapping) -> Non
         raise RuntimeError("Paged KV HIP Store: slot_mapping must hold one slot per token")
 
 
+def _stream_of(index: int) -> int:
+    """The current stream of GPU ``index`` as a hipStream_t integer."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+def store_checked(key, value, key_cache, value_cache, slot_mapping) -> None:
+    """The store launch for inputs that already meet the store contract
+    (the backend's validator, or the op's own checks): one GPU, matching
+    shapes and dtypes, a contiguous int32 slot_mapping with one slot per
+    token.  What remains is what only the kernel needs: contiguous caches,
+    a contiguous row per token, a dtype it moves."""
+    if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
+        raise ValueError("paged KV HIP Store requires contiguous [blocks, block, kv_heads, "
+                         "head_dim] caches")
+    shape = key.shape
+    num_tokens = shape[0]
+    if num_tokens == 0:
+        return
+    code = DTYPE_CODES.get(key.dtype)
+    if code is None:
+        dtype_code(key.dtype)  # raises with the supported dtypes
+    # The kernel addresses a token's [kv_heads, head_dim] as one contiguous
+    # row through the token stride.  A head-strided view (e.g. kv[:, :, :128]
+    # of a [T, H, 256] tensor) passes the validators, which only require a
+    # contiguous last dimension, so it is compacted on the device first.
+    kstride = key.stride()
+    if shape[1] > 1 and kstride[1] != shape[2]:
+        key = key.contiguous()
+        kstride = key.stride()
+    vstride = value.stride()
+    if shape[1] > 1 and vstride[1] != shape[2]:
+        value = value.contiguous()
+        vstride = value.stride()
+    cshape = key_cache.shape
+    status = _lib.load_library().nkv_store(
+        key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+        slot_mapping.data_ptr(), num_tokens, kstride[0], vstride[0], shape[1] * shape[2],
+        cshape[0] * cshape[1], code, _stream_of(key.get_device()),
+    )
+    if status:
+        _lib.check(status, "nanovllm_paged_kv::store")
+
+
+def gather_checked(cache, block_table, sequence_length: int) -> torch.Tensor:
+    """The gather launch for inputs that already meet the gather contract
+    (a 4-D cache and a contiguous 1-D int32 table on one GPU, covering the
+    length).  Returns a new [sequence_length, kv_heads, head_dim] tensor of
+    the cache's dtype on its device."""
+    if not cache.is_contiguous():
+        raise ValueError("paged KV HIP Gather requires contiguous [blocks, block, kv_heads, "
+                         "head_dim] caches")
+    num_blocks, block_size, heads, head_dim = cache.shape
+    out = cache.new_empty((sequence_length, heads, head_dim))
+    if sequence_length == 0:
+        return out
+    code = DTYPE_CODES.get(cache.dtype)
+    if code is None:
+        dtype_code(cache.dtype)  # raises with the supported dtypes
+    status = _lib.load_library().nkv_gather(
+        cache.data_ptr(), block_table.data_ptr(), block_table.shape[0], sequence_length,
+        block_size, heads * head_dim, num_blocks, code, out.data_ptr(),
+        _stream_of(cache.get_device()),
+    )
+    if status:
+        _lib.check(status, "nanovllm_paged_kv::gather")
+    return out
+
+
 def _store_impl(key, value, key_cache, value_cache, slot_mapping) -> None:
-    device = _require_device("paged KV HIP Store", key, value, key_cache, value_cache, slot_mapping)
+    _require_device("paged KV HIP Store", key, value, key_cache, value_cache, slot_mapping)
     _require_contiguous_cache("paged KV HIP Store", key_cache, value_cache)
     if key.dtype != value.dtype or key.dtype != key_cache.dtype or key.dtype != value_cache.dtype:
         raise RuntimeError("Paged KV HIP Store dtype mismatch")
     slot_mapping = _int32_index("Paged KV HIP Store", "slot_mapping", slot_mapping)
     _require_store_rows(key, value, key_cache, value_cache, slot_mapping)
-    num_tokens = key.shape[0]
-    if num_tokens == 0:
-        return
-    # The kernel addresses a token's [kv_heads, head_dim] as one contiguous
-    # row through the token stride.  A head-strided view (e.g. kv[:, :, :128]
-    # of a [T, H, 256] tensor) passes the validators, which only require a
-    # contiguous last dimension, so it is compacted on the device first.
-    if key.shape[1] > 1 and key.stride(1) != key.shape[2]:
-        key = key.contiguous()
-    if value.shape[1] > 1 and value.stride(1) != value.shape[2]:
-        value = value.contiguous()
-    library = _lib.load_library()
-    status = library.nkv_store(
-        key.data_ptr(),
-        value.data_ptr(),
-        key_cache.data_ptr(),
-        value_cache.data_ptr(),
-        slot_mapping.data_ptr(),
-        num_tokens,
-        key.stride(0),
-        value.stride(0),
-        key.shape[1] * key.shape[2],
-        key_cache.shape[0] * key_cache.shape[1],
-        dtype_code(key.dtype),
-        _stream(device),
-    )
-    _lib.check(status, "nanovllm_paged_kv::store")
+    store_checked(key, value, key_cache, value_cache, slot_mapping)
 
 
 def _gather_impl(cache, block_table, sequence_length: int) -> torch.Tensor:
-    device = _require_device("paged KV HIP Gather", cache, block_table)
+    _require_device("paged KV HIP Gather", cache, block_table)
     _require_contiguous_cache("paged KV HIP Gather", cache)
     block_table = _int32_index("Paged KV HIP Gather", "block_table", block_table)
-    num_blocks, block_size, heads, head_dim = cache.shape
-    out = torch.empty((sequence_length, heads, head_dim), dtype=cache.dtype, device=device)
-    if sequence_length == 0:
-        return out
-    status = _lib.load_library().nkv_gather(
-        cache.data_ptr(),
-        block_table.data_ptr(),
-        block_table.numel(),
-        sequence_length,
-        block_size,
-        heads * head_dim,
-        num_blocks,
-        dtype_code(cache.dtype),
-        out.data_ptr(),
-        _stream(device),
-    )
-    _lib.check(status, "nanovllm_paged_kv::gather")
-    return out
+    if cache.ndim != 4 or block_table.ndim != 1:
+        raise RuntimeError("Paged KV HIP Gather: cache must be [blocks, block, kv_heads, head_dim] "
+                           "and block_table one-dimensional")
+    return gather_checked(cache, block_table, sequence_length)
 
 
 def _build_plan_impl(
