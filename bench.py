@@ -58,7 +58,7 @@ METRIC = "paged KV store+gather GB/s (fraction of HBM peak); decode-step tokens/
 # with paged-attention decode in place of the gather.
 PROFILE_CASES = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows", "decode_step",
                  "decode_attention", "grouped_decode_2x8", "grouped_decode_4x7", "grouped_decode_8x4",
-                 "prefill_attention", "block_pool")
+                 "prefill_attention", "block_pool", "store_floor")
 
 
 PROFILE_FILE = REPO_ROOT / "profiles" / "decode_step_rocprof.json"
@@ -229,6 +229,12 @@ def main(argv=None) -> int:
 
         replay_workload(args.case, args.profile_replay, device)
         print(f"profile replay complete: {args.case} x {args.profile_replay}", flush=True)
+        return 0
+    if args.case == "store_floor":
+        from nanokv.benchmark import replay_store_floor
+
+        replay_store_floor(args.profile_replay, device)
+        print(f"profile replay complete: store_floor x {args.profile_replay}", flush=True)
         return 0
     if args.case in GROUPED_CASES:
         from nanokv import workloads

@@ -473,6 +473,47 @@ def replay_workload(name: str, replays: int, device=None) -> None:
     torch.cuda.synchronize(device)
 
 
+def replay_store_floor(replays: int, device=None) -> None:
+    """The chunked-prefill store beside what bounds it, for a profiler:
+    ``replays`` launches each, in this order, of (1) torch's ``copy_`` of a
+    32 MiB bf16 tensor, 67,108,864 bytes moved, what the store of 8,192 rows
+    of 2 KiB of K and V moves; (2) the store of 8,192 K/V rows into slots
+    0..8191 (32 consecutive blocks); (3) the same rows into the
+    chunked-prefill workload's slots (blocks scattered over the 2 GiB
+    caches).  A 512 MiB read precedes every launch, as in the workload
+    replay.  Nothing else launches the store kernel, so a trace splits its
+    dispatches between (2) and (3) by order; both stores' results are
+    checked bit-exactly by the GPU parity tests, not here."""
+    from nanokv import workloads
+    from nanokv.paged_kv import create_paged_kv_backend
+
+    device = device or torch.device("cuda", 0)
+    backend = create_paged_kv_backend("hip")
+    wl = workloads.build("chunked_prefill")
+    shape = (wl.num_blocks, wl.block_size, wl.num_kv_heads, wl.head_dim)
+    g = torch.Generator(device=device).manual_seed(23)
+    key_cache = torch.randn(shape, generator=g, device=device).to(wl.dtype)
+    value_cache = torch.randn(shape, generator=g, device=device).to(wl.dtype)
+    rows = (wl.slot_mapping.size, wl.num_kv_heads, wl.head_dim)
+    key = torch.randn(rows, generator=g, device=device).to(wl.dtype)
+    value = torch.randn(rows, generator=g, device=device).to(wl.dtype)
+    contiguous = torch.arange(rows[0], dtype=torch.int32, device=device)
+    scattered = torch.from_numpy(wl.slot_mapping).to(device)
+    src = torch.randn(key.numel() * 2, generator=g, device=device).to(wl.dtype)
+    dst = torch.empty_like(src)
+    assert 2 * src.numel() * src.element_size() == 67_108_864
+    ops = (lambda: dst.copy_(src),
+           lambda: backend.store(key, value, key_cache, value_cache, contiguous),
+           lambda: backend.store(key, value, key_cache, value_cache, scattered))
+    flush = torch.zeros(FLUSH_BYTES, dtype=torch.uint8, device=device).view(torch.int64)
+    torch.cuda.synchronize(device)
+    for op in ops:
+        for _ in range(replays):
+            flush.sum()
+            op()
+    torch.cuda.synchronize(device)
+
+
 def render_markdown(records: list[dict]) -> str:
     lines = ["| Workload | Operation | Algorithmic bytes | p50 (us) | p95 (us) | GB/s at p50 | HBM fraction |",
              "|---|---|---:|---:|---:|---:|---:|"]

@@ -46,7 +46,32 @@ from typing import Iterable, Sequence
 HBM_PEAK_GBPS = 8000.0
 CASES = ("decode_store", "chunked_prefill", "prefix_gather", "narrow_rows", "decode_step",
          "decode_attention", "grouped_decode_2x8", "grouped_decode_4x7", "grouped_decode_8x4",
-         "prefill_attention", "block_pool")
+         "prefill_attention", "block_pool", "store_floor")
+# Cases whose replay launches one kernel in consecutive phases: that
+# kernel's dispatches are split evenly among the labels by dispatch order.
+PHASES = {"store_floor": {"store_rows_kernel": ("contiguous slots", "chunked-prefill slots")}}
+# Runtime kernels a case reports beside its own (the kernel torch's copy_
+# runs for a device-to-device copy).  Only their dispatches of the most
+# frequent grid are kept: the replay's own launches, not the runtime's
+# setup copies of other sizes.
+EXTRA_KERNELS = {"store_floor": ("__amd_rocclr_copyBuffer",)}
+
+
+def modal_grid_only(dispatches: Sequence[Dispatch], prefixes: Sequence[str]) -> list[Dispatch]:
+    """Drop the dispatches of kernels named by ``prefixes`` whose grid is not
+    the kernel's most frequent grid."""
+    keep = _modal_grids([(d.kernel, d.grid) for d in dispatches], prefixes)
+    return [d for d in dispatches if not d.kernel.startswith(tuple(prefixes))
+            or keep.get(d.kernel) == d.grid]
+
+
+def _modal_grids(pairs, prefixes) -> dict:
+    counts: dict = {}
+    for kernel, grid in pairs:
+        if kernel.startswith(tuple(prefixes)):
+            counts.setdefault(kernel, {}).setdefault(grid, 0)
+            counts[kernel][grid] += 1
+    return {k: max(v.items(), key=lambda kv: kv[1])[0] for k, v in counts.items()}
 GROUPED = {"grouped_decode_2x8": (2, 8), "grouped_decode_4x7": (4, 7), "grouped_decode_8x4": (8, 4)}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 COPY_CALIBRATION_MIB = 1024
@@ -233,6 +258,35 @@ def read_kernel_trace(path: str | Path) -> list[Dispatch]:
     return out
 
 
+def label_phases(dispatches: Sequence[Dispatch], phases: dict[str, Sequence[str]]) -> list[Dispatch]:
+    """Rename the dispatches of each kernel named in ``phases`` (by short-name
+    prefix) to ``"<name> [<label>]"``, the labels taken in dispatch order,
+    an equal share of the dispatches each."""
+    out = list(dispatches)
+    for prefix, labels in phases.items():
+        picked = [i for i, d in enumerate(out) if d.kernel.startswith(prefix)]
+        per = max(1, len(picked) // len(labels))
+        for j, i in enumerate(picked):
+            label = labels[min(j // per, len(labels) - 1)]
+            d = out[i]
+            out[i] = Dispatch(f"{d.kernel} [{label}]", d.dispatch_id, d.start_ns, d.end_ns, d.grid,
+                              d.workgroup)
+    return out
+
+
+def label_counter_phases(rows: Sequence[dict], phases: dict[str, Sequence[str]]) -> list[dict]:
+    """:func:`label_phases` for counter rows (one or more rows per dispatch)."""
+    out = [dict(r) for r in rows]
+    for prefix, labels in phases.items():
+        ids = sorted({r["dispatch_id"] for r in out if r["kernel"].startswith(prefix)})
+        per = max(1, len(ids) // len(labels))
+        rank = {d: labels[min(j // per, len(labels) - 1)] for j, d in enumerate(ids)}
+        for r in out:
+            if r["dispatch_id"] in rank and r["kernel"].startswith(prefix):
+                r["kernel"] = f"{r['kernel']} [{rank[r['dispatch_id']]}]"
+    return out
+
+
 def _percentile(sorted_values: Sequence[float], q: float) -> float:
     position = (len(sorted_values) - 1) * q
     lo = int(position)
@@ -273,6 +327,7 @@ def read_counters(path: str | Path) -> list[dict]:
         for row in csv.DictReader(handle):
             out.append({"kernel": short_name(row["Kernel_Name"]),
                         "dispatch_id": int(row["Dispatch_Id"]),
+                        "grid": int(row.get("Grid_Size") or 0),
                         "counter": row["Counter_Name"].strip(),
                         "value": float(row["Counter_Value"])})
     return out
@@ -321,19 +376,27 @@ def summarize(case: str, out: Path, algorithmic_bytes: dict[str, int], *,
     trace statistics, the achieved bandwidth on its median duration
     (algorithmic bytes per launch from ``algorithmic_bytes``, keyed by a
     prefix of the short kernel name) and the calibrated HBM traffic."""
-    trace = kernel_durations(read_kernel_trace(_find_csv(out / "trace", "_kernel_trace.csv")),
-                             skip_first=skip_first)
+    phases = PHASES.get(case, {})
+    extra = EXTRA_KERNELS.get(case, ())
+    trace = kernel_durations(
+        label_phases(modal_grid_only(read_kernel_trace(_find_csv(out / "trace", "_kernel_trace.csv")),
+                                     extra), phases),
+        skip_first=skip_first)
     factors, traffic = {}, {}
     for counter, key in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write")):
         copy_dir, case_dir = out / f"copy_{key}", out / key
         if copy_dir.is_dir() and case_dir.is_dir():
             factors[counter] = copy_factor(read_counters(_find_csv(copy_dir, "_counter_collection.csv")),
                                            counter)
-            traffic[counter] = counter_means(
-                read_counters(_find_csv(case_dir, "_counter_collection.csv")), counter)
+            rows = read_counters(_find_csv(case_dir, "_counter_collection.csv"))
+            keep = _modal_grids([(r["kernel"], r["grid"]) for r in rows], extra)
+            rows = [r for r in rows if not r["kernel"].startswith(tuple(extra))
+                    or keep.get(r["kernel"]) == r["grid"]]
+            traffic[counter] = counter_means(label_counter_phases(rows, phases), counter)
+    reported = ("nkv", "store_", "gather_", "build_", "pack_", "attn_", "pool_", *extra)
     kernels = {}
     for name, stats in sorted(trace.items(), key=lambda kv: -kv[1]["median_us"] * kv[1]["dispatches"]):
-        if not (name.startswith(("nkv", "store_", "gather_", "build_", "pack_", "attn_", "pool_"))):
+        if not name.startswith(reported):
             continue
         record = dict(stats)
         nbytes = next((b for prefix, b in algorithmic_bytes.items() if name.startswith(prefix)), None)
@@ -357,6 +420,8 @@ def summarize(case: str, out: Path, algorithmic_bytes: dict[str, int], *,
             record["traffic_bytes"] = round(moved["FETCH_SIZE"] + moved["WRITE_SIZE"])
             if nbytes:
                 record["traffic_over_algorithmic"] = record["traffic_bytes"] / nbytes
+            # the rate in bytes that actually crossed the HBM interface
+            record["hbm_gbps_at_median"] = record["traffic_bytes"] / (stats["median_us"] * 1e3)
         kernels[name] = record
     return {
         "schema_version": "nanokv.rocprof_summary.v1",
@@ -404,14 +469,19 @@ def render_markdown(summary: dict, title: str | None = None) -> str:
                   f"{COPY_CALIBRATION_MIB} MiB (`{COPY_KERNEL}`): FETCH_SIZE reads "
                   f"{f.get('FETCH_SIZE', float('nan')):.4f}x and WRITE_SIZE "
                   f"{f.get('WRITE_SIZE', float('nan')):.4f}x the true bytes.", "",
-                  "| Kernel | HBM read (B) | HBM written (B) | Total (B) | Algorithmic (B) | Ratio |",
-                  "|---|---:|---:|---:|---:|---:|"]
+                  "The last two columns are the rate in counter bytes (what crossed the HBM "
+                  "interface) over the median duration, and its fraction of peak.", "",
+                  "| Kernel | HBM read (B) | HBM written (B) | Total (B) | Algorithmic (B) | Ratio "
+                  "| HBM GB/s at median | % of peak |",
+                  "|---|---:|---:|---:|---:|---:|---:|---:|"]
         for name, k in summary["kernels"].items():
             if "traffic_bytes" in k:
                 alg = k.get("algorithmic_bytes")
+                hbm = k["traffic_bytes"] / (k["median_us"] * 1e3)
                 lines.append(f"| `{name}` | {k['hbm_read_bytes']:,} | {k['hbm_write_bytes']:,} | "
                              f"{k['traffic_bytes']:,} | " + (f"{alg:,} | {k['traffic_over_algorithmic']:.3f} |"
-                                                              if alg else "— | — |"))
+                                                              if alg else "— | — |")
+                             + f" {hbm:,.0f} | {100 * hbm / summary['peak_gbps']:.1f}% |")
     return "\n".join(lines) + "\n"
 
 
@@ -454,6 +524,9 @@ def algorithmic_bytes_for(case: str) -> dict[str, int]:
         return {"attn_decode_mfma_kernel": total * hkv * 128 * 2 * 2 + 2 * q_bytes}
     if case in ("prefill_attention", "block_pool"):
         return {}
+    if case == "store_floor":
+        wl = workloads.build("chunked_prefill")
+        return {"__amd_rocclr_copyBuffer": 67_108_864, "store_rows_kernel": wl.store_bytes(layers=1)}
     wl = workloads.build(case, num_layers=1) if case == "decode_step" else workloads.build(case)
     found = {}
     if wl.slot_mapping is not None:

@@ -256,3 +256,46 @@ def test_trace_on_this_host_echoes_the_child(tmp_path, monkeypatch, capsys):
                                       timeout_s=60, echo=True)
     assert "error" not in got
     assert "[trace] profile replay complete: decode_step" in capsys.readouterr().err
+
+
+def test_store_floor_phases_split_one_kernel_by_dispatch_order(tmp_path):
+    """The store-floor replay launches the copy, then the store into
+    contiguous slots, then into the workload's slots: the store's dispatches
+    are labelled by order (first half, second half), trace and counters
+    alike, and the copy is reported beside them with its own bytes."""
+    out = tmp_path / "store_floor"
+    for d in ("trace", "fetch", "write", "copy_fetch", "copy_write"):
+        (out / d).mkdir(parents=True)
+    dispatches = [(COPY, 0, 12_000)] * 3 + [(STORE, 0, 12_100)] * 3 + [(STORE, 0, 13_700)] * 3
+    write_trace(out / "trace" / "t_kernel_trace.csv", dispatches)
+    # a setup copy of another size before the replay: dropped (not the copy's modal grid)
+    with open(out / "trace" / "t_kernel_trace.csv", newline="") as handle:
+        rows = list(csv.DictReader(handle))
+    setup = dict(rows[0], Dispatch_Id=0, End_Timestamp=900_000, Grid_Size_X=999_424)
+    with open(out / "trace" / "t_kernel_trace.csv", "w", newline="") as handle:
+        w = csv.DictWriter(handle, TRACE_COLUMNS)
+        w.writeheader()
+        w.writerows([setup] + rows)
+    mib = 1024 * 1024
+    write_counters(out / "copy_fetch" / "c_counter_collection.csv", [(1, COPY, "FETCH_SIZE", 512 * 1024)])
+    write_counters(out / "copy_write" / "c_counter_collection.csv", [(1, COPY, "WRITE_SIZE", 1024 * 1024)])
+    fetch = [(i, COPY, "FETCH_SIZE", 16 * 1024) for i in (1, 2, 3)]
+    fetch += [(i, STORE, "FETCH_SIZE", 16 * 1024) for i in (4, 5, 6)]
+    fetch += [(i, STORE, "FETCH_SIZE", 17 * 1024) for i in (7, 8, 9)]
+    write_counters(out / "fetch" / "f_counter_collection.csv", fetch)
+    write = [(i, COPY if i < 4 else STORE, "WRITE_SIZE", 32 * 1024) for i in range(1, 10)]
+    write_counters(out / "write" / "w_counter_collection.csv", write)
+    summary = profiling.summarize("store_floor", out, profiling.algorithmic_bytes_for("store_floor"))
+    k = summary["kernels"]
+    contiguous, scattered = ("store_rows_kernel<16> [contiguous slots]",
+                             "store_rows_kernel<16> [chunked-prefill slots]")
+    assert set(k) == {"__amd_rocclr_copyBuffer", contiguous, scattered}
+    assert k[contiguous]["dispatches"] == 2 and k[contiguous]["median_us"] == pytest.approx(12.1)
+    assert k[scattered]["median_us"] == pytest.approx(13.7)
+    assert k["__amd_rocclr_copyBuffer"]["algorithmic_bytes"] == 67_108_864
+    assert k["__amd_rocclr_copyBuffer"]["dispatches"] == 2          # 3 replayed, first skipped
+    assert k["__amd_rocclr_copyBuffer"]["max_us"] == pytest.approx(12.0)
+    assert k[contiguous]["hbm_read_bytes"] == 32 * mib and k[scattered]["hbm_read_bytes"] == 34 * mib
+    assert k[scattered]["hbm_gbps_at_median"] == pytest.approx(66 * mib / 13_700)
+    text = profiling.render_markdown(summary)
+    assert "[contiguous slots]" in text and "HBM GB/s at median" in text
