@@ -32,8 +32,9 @@ single-layer store / gather configurations (decode store, chunked-prefill
 store, prefix-cache gather, narrow rows) kernel by kernel; "gpu_reference"
 runs the reference pytorch backend's torch ops on the same GPU, on the
 decode step and on the reference's own store/gather microbenchmark matrix;
-"prefill_attention" times the causal paged prefill kernel on the
-chunked-prefill step against the reference's SDPA prefill path;
+"prefill_attention" (with --prefill-attention) times the causal paged
+prefill kernel on the chunked-prefill step against the reference's SDPA
+prefill path;
 "grouped_decode_attention" times one decode-attention layer over the same
 contexts for the grouped-query layouts of Qwen2.5-VL-3B / -7B and
 Qwen3-VL-8B (the MFMA decode kernel).
@@ -121,6 +122,9 @@ def parse_args(argv=None):
     p.add_argument("--prefill-only", action="store_true",
                    help="only time the paged prefill attention on the chunked-prefill step "
                         "(and its SDPA-path baseline), print that record, then exit")
+    p.add_argument("--prefill-attention", action="store_true",
+                   help="also time the paged prefill attention in the default run (off by default: "
+                        "prefill attention is outside the store/gather path)"),
     p.add_argument("--copy-calibration-mib", type=int, default=0,
                    help="only run a plain device copy of this many MiB 3 times (the known-size "
                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
@@ -507,6 +511,9 @@ def main(argv=None) -> int:
         log(f"[bench] WARNING: {L} x {gather_launch_us:.1f} us of back-to-back gathers exceed the "
             f"{step_ms:.3f} ms step")
     profiled = profiled_median(PROFILE_FILE, "gather_planned_kernel", gather_launch_bytes)
+    same_host = same_host_roofline(same_host_trace, gather_launch_bytes, gather_launch_us)
+    same_host_frac = (round(gather_launch_bytes / (same_host["median_us"] * 1e3) / MI355X_HBM_PEAK_GBPS, 4)
+                      if same_host and "median_us" in same_host else None)
 
     fused_step = measure_fused_step(wl, device, backend, packer, batch, cache, new_k, new_v, total,
                                     k_out, v_out, args.steps, args.warmup)
@@ -523,7 +530,7 @@ def main(argv=None) -> int:
         f"{block_pool['stream_us_per_step']:.1f} us stream / {block_pool['host_us_per_step']:.1f} us host")
 
     prefill_attention = None
-    if not args.profile:
+    if args.prefill_attention and not args.profile:
         prefill_attention = measure_prefill_attention(device, backend, args.steps)
         log(f"[bench] prefill attention (chunked prefill, 8192 tokens): "
             f"{prefill_attention['us']:.1f} us, {prefill_attention['tflops']:.0f} TFLOP/s, "
@@ -649,10 +656,14 @@ def main(argv=None) -> int:
                       f"pair around them, on the stream the kernel runs on",
             "launches_per_step_us": round(L * gather_launch_us, 1),
             "within_step": consistent,
+            "timing_source": "hip events around the back-to-back launches (achieved, frac, "
+                             "us_per_launch); the rocprofv3 figures of the same kernel follow",
+            "frac_rocprof_same_host": same_host_frac,
             "rocprof_median_us": profiled,
+            "frac_rocprof_committed": (round(gather_launch_bytes / (profiled * 1e3)
+                                             / MI355X_HBM_PEAK_GBPS, 4) if profiled else None),
             "rocprof_source": str(PROFILE_FILE.relative_to(REPO_ROOT)) if profiled else None,
-            "rocprof_same_host": same_host_roofline(same_host_trace, gather_launch_bytes,
-                                                    gather_launch_us),
+            "rocprof_same_host": same_host,
         },
         "attention": {
             "kernel": "paged_attention_decode (split-K partials + merge, one layer, 16 q heads "
@@ -1573,8 +1584,10 @@ def cpu_reference_baseline(wl, layers: int, workload_names) -> dict:
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "ops": "reference pytorch backend torch ops: index_copy_ store, index_select gather "
-               "(nanovllm/layers/paged_kv/pytorch_backend.py:26-50), validators included",
+        "ops": "the reference's pytorch backend (nanovllm/layers/paged_kv/pytorch_backend.py:26-50) "
+               "ported line for line: its validators, then its own torch ops (index_copy_ store, "
+               "index_select gather) on host tensors; a port of the reference's Python code, which "
+               "is read here, not imported",
         "sample": (f"decode step: {layers} of the 28 layers (store of the 256 new rows, then 256 x 2 "
                    f"per-sequence gathers of K and V) on host tensors, one layer-sized cache, "
                    f"{per_layer:.2f} s per layer"),

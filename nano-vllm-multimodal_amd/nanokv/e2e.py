@@ -47,7 +47,9 @@ from nanokv.benchmark import linear_percentile
 ORACLE_BACKEND = "pytorch"
 BACKEND_NAMES = ("pytorch", "triton", "cuda", "hip")
 GENERATION_STAGES = ("native-sdpa", "native-flash")
-SCHEMA = "nanokv.paged_kv_e2e_comparison.v1"
+# The reference's schema id (paged_kv_e2e.py:87): the result carries the
+# reference's field names, so a consumer that keys on the id reads it.
+SCHEMA = "nanoinfer.paged_kv_e2e_comparison.v1"
 
 
 @dataclass(frozen=True)
@@ -94,6 +96,16 @@ def _problems_of(backend: str, report: Any) -> list[str]:
                        if k not in case["benchmark"]]
             if missing:
                 found.append(f"{backend}: case {name!r} benchmark lacks {', '.join(missing)}")
+                continue
+            try:
+                latency = float(case["benchmark"]["total_latency_sec"])
+            except (TypeError, ValueError):
+                latency = float("nan")
+            # the reference's latency summary rejects negative samples
+            # (benchmark/paged_kv.py:202-205)
+            if not latency >= 0.0:
+                found.append(f"{backend}: case {name!r} total_latency_sec must be a "
+                             f"non-negative number, got {case['benchmark']['total_latency_sec']!r}")
     return found
 
 

@@ -55,8 +55,9 @@ class HIPPagedKVCache:
         return len(self._pending)
 
     def pending_host_copy_count(self) -> int:
-        """Host tensors still retained (paged_kv.cpp:268-270): completed
-        copies are released lazily, at the next copy_slots_async."""
+        """Host tensors still retained (paged_kv.cpp:97-99): completed
+        copies are released lazily, at the next copy_slots_async (which
+        starts with release_completed_host_copies, paged_kv.cpp:110,156-167)."""
         with self._lock:
             return len(self._pending)
 

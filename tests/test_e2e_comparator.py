@@ -128,3 +128,17 @@ def test_command_line_writes_json_and_markdown(tmp_path, capsys):
     assert json.loads((out / "paged-kv-e2e-comparison.json").read_text())["divergences"]
     with pytest.raises(SystemExit):
         main(["--hip", str(paths["hip"])])
+
+
+def test_negative_or_missing_latency_is_rejected_and_schema_is_the_reference_id():
+    """A negative (or non-numeric) case latency is a report problem, as the
+    reference's latency summary rejects negative samples
+    (benchmark/paged_kv.py:202-205); the result carries the reference's
+    schema id (paged_kv_e2e.py:87), whose field names it uses."""
+    for latency in (-0.5, "fast", None):
+        bad = generation_report("hip", (1.0, latency, 2.0))
+        with pytest.raises(ValueError, match="'two-images' total_latency_sec must be a non-negative"):
+            parse_run("hip", bad)
+    result = compare_paged_kv_reports({"pytorch": generation_report("pytorch", (1.0, 2.0, 0.0)),
+                                       "hip": generation_report("hip", (0.5, 1.0, 0.0))})
+    assert result["schema_version"] == "nanoinfer.paged_kv_e2e_comparison.v1"

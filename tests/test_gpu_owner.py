@@ -70,7 +70,7 @@ def test_async_copy_retains_ephemeral_pinned_host_tensor(backend):
     gc.collect()
     torch.cuda.current_stream().synchronize()
     assert device_slots.tolist() == [0, 3, 7]
-    # Completed copies are released at the next upload (paged_kv.cpp:280).
+    # Completed copies are released at the next upload (paged_kv.cpp:110,156-167).
     backend.copy_slots_async(allocation, torch.tensor([1], dtype=torch.int32).pin_memory())
     assert allocation.owner.pending_host_copy_count() <= 1
 

@@ -148,3 +148,108 @@ def test_noalloc_plan_that_fills_the_scratch(gpu_device):
     assert b"scratch" in lib.nkv_last_error()
     torch.cuda.synchronize(gpu_device)
     assert (k_out.view(torch.int16) == SENTINEL).all()
+
+
+def test_noalloc_allocates_nothing_on_later_calls(gpu_device):
+    """After a first call (which loads the kernels and the array with the
+    library's code object), calls change neither the device's free memory
+    nor torch's allocations."""
+    lib = _lib.load_library()
+    rng = np.random.default_rng(99)
+    case = _case(rng, 37, 2000, 256, 8, 128, torch.bfloat16, gpu_device)
+    k_out, v_out = _outputs(case, gpu_device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(gpu_device).cuda_stream)
+    args = (case["kc"].data_ptr(), case["vc"].data_ptr(), case["d_tables"].data_ptr(),
+            case["d_tables"].shape[1], case["d_cu"].data_ptr(), 37, case["total"],
+            256, 1024, case["num_blocks"], _lib.NKV_DTYPE_BFLOAT16, k_out.data_ptr(),
+            v_out.data_ptr(), stream)
+    _lib.check(lib.nkv_gather_varlen_noalloc(*args), "nkv_gather_varlen_noalloc")
+    torch.cuda.synchronize(gpu_device)
+    free_before, _ = torch.cuda.mem_get_info(gpu_device)
+    allocated_before = torch.cuda.memory_allocated(gpu_device)
+    for _ in range(5):
+        _lib.check(lib.nkv_gather_varlen_noalloc(*args), "nkv_gather_varlen_noalloc")
+    torch.cuda.synchronize(gpu_device)
+    assert torch.cuda.mem_get_info(gpu_device)[0] == free_before
+    assert torch.cuda.memory_allocated(gpu_device) == allocated_before
+
+
+# Run in a fresh interpreter, so that the entry point's first call on the
+# device (its one-time scratch address lookup) happens inside the capture.
+GRAPH_CHILD = r'''
+import ctypes, sys
+import numpy as np
+import torch
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+from nanokv import _lib
+lib = _lib.load_library()
+dev = torch.device("cuda", 0)
+rng = np.random.default_rng(5)
+bs, heads, dim, seqs = 16, 2, 128, 23
+lens = rng.integers(0, 400, seqs)
+need = -(-lens // bs)
+nb = int(need.sum()) + 4
+perm = rng.permutation(nb).astype(np.int32)
+tables = np.full((seqs, int(need.max()) + 1), -1, np.int32)
+c = 0
+for i, n in enumerate(need.tolist()):
+    tables[i, :n] = perm[c:c + n]
+    c += n
+cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+total = int(cu[-1])
+kc = torch.randn(nb, bs, heads, dim, device=dev).to(torch.bfloat16)
+vc = torch.randn_like(kc)
+d_tables, d_cu = torch.from_numpy(tables).to(dev), torch.from_numpy(cu).to(dev)
+k_out = torch.empty(total, heads, dim, dtype=torch.bfloat16, device=dev)
+v_out = torch.empty_like(k_out)
+cap = lib.nkv_gather_plan_capacity(total, seqs, bs, heads * dim, _lib.NKV_DTYPE_BFLOAT16)
+workspace = torch.empty(16 * cap, dtype=torch.uint8, device=dev)
+
+def call(entry, stream, ko, vo, *extra):
+    args = (kc.data_ptr(), vc.data_ptr(), d_tables.data_ptr(), tables.shape[1], d_cu.data_ptr(),
+            seqs, total, bs, heads * dim, nb, _lib.NKV_DTYPE_BFLOAT16, ko.data_ptr(), vo.data_ptr())
+    _lib.check(entry(*args, *extra, ctypes.c_void_p(stream)), "call")
+
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+side = torch.cuda.Stream()
+with torch.cuda.graph(graph, stream=side):
+    call(lib.nkv_gather_varlen_noalloc, side.cuda_stream, k_out, v_out)
+expect_k, expect_v = torch.empty_like(k_out), torch.empty_like(v_out)
+for replay in range(4):
+    kc.copy_(torch.randn(kc.shape, device=dev).to(torch.bfloat16))   # eager work between replays
+    vc.copy_(torch.randn(vc.shape, device=dev).to(torch.bfloat16))
+    k_out.fill_(0)
+    v_out.fill_(0)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    call(lib.nkv_gather_varlen, torch.cuda.current_stream().cuda_stream, expect_k, expect_v,
+         workspace.data_ptr(), workspace.numel())
+    torch.cuda.synchronize()
+    same = (torch.equal(k_out.view(torch.int16), expect_k.view(torch.int16))
+            and torch.equal(v_out.view(torch.int16), expect_v.view(torch.int16)))
+    print(f"replay {replay}: {'equal' if same else 'DIFFERENT'} ({total} rows)", flush=True)
+    if not same:
+        sys.exit(1)
+print("graph ok", flush=True)
+'''
+
+
+def test_noalloc_first_call_under_graph_capture(gpu_device):
+    """A fresh process whose first call of the entry point is made while a
+    graph is being captured; the graph is replayed four times, with eager
+    work and synchronisations between the replays, each replay bit-exact
+    against the workspace entry point on the same (changed) caches."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    print("[no-alloc] graph capture in a fresh process", flush=True)
+    done = subprocess.run([sys.executable, "-c", GRAPH_CHILD, str(root),
+                           str(root / "nano-vllm-multimodal_amd")],
+                          capture_output=True, text=True, timeout=180)
+    print(done.stdout[-2000:], done.stderr[-2000:], flush=True)
+    assert done.returncode == 0
+    assert done.stdout.count("equal") == 4 and "graph ok" in done.stdout
