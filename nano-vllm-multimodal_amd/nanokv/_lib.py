@@ -237,6 +237,46 @@ def load_library() -> ctypes.CDLL:
     return _LIBRARY
 
 
+_HOST_LOCK = Lock()
+_HOST = None
+
+
+def load_host():
+    """The C++ host binding of the backend's per-call store and gather
+    (``nanokv._nkv_host``), bound to the loaded library's entry points.  A
+    missing or stale binding raises RuntimeError: there is no slower path
+    to fall back to silently."""
+    global _HOST
+    if _HOST is not None:
+        return _HOST
+    library = load_library()
+    with _HOST_LOCK:
+        if _HOST is None:
+            import importlib
+
+            try:
+                module = importlib.import_module("nanokv._nkv_host")
+            except ImportError as exc:
+                raise RuntimeError(
+                    f"nanokv host binding not built or not loadable ({_build.host_module_path()}: "
+                    f"{exc}); run __graft_entry__.build() or python -m nanokv.build") from exc
+            source = _build.SOURCE_DIR / _build.HOST_SOURCE
+            if source.is_file() and (_build.INCLUDE_DIR / "nanokv.h").is_file():
+                expected = _build.host_build_id()
+                if module.build_id() != expected:
+                    raise RuntimeError(
+                        f"{module.__file__} is stale: built as {module.build_id()!r}, the sources "
+                        f"and this torch give {expected!r}; rebuild it (__graft_entry__.build() or "
+                        "python -m nanokv.build)")
+
+            def address(name: str) -> int:
+                return ctypes.cast(getattr(library, name), ctypes.c_void_p).value
+
+            module.bind(address("nkv_store"), address("nkv_gather"), address("nkv_last_error"))
+            _HOST = module
+    return _HOST
+
+
 def build_id() -> str:
     """nkv_build_id() of the loaded library: the fingerprint of the sources
     it was built from and its launch-shape config."""

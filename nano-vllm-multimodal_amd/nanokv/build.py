@@ -157,6 +157,84 @@ def build(*, verbose: bool = False, output: Path | None = None,
     return target
 
 
+# ------------------------------------------------------------ host binding
+#
+# _nkv_host: the backend's per-call store / gather path in C++ (csrc/
+# nkv_host.cpp), a CPython extension compiled with g++ against torch's
+# headers (it has no device code).  It is bound to the torch it was built
+# against, so torch's version is part of its fingerprint.
+
+HOST_SOURCE = "nkv_host.cpp"
+HOST_FLAGS = ("-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-unused-function")
+
+
+def host_module_path() -> Path:
+    import sysconfig
+
+    return PACKAGE_DIR / f"_nkv_host{sysconfig.get_config_var('EXT_SUFFIX')}"
+
+
+def host_build_id(source_dir: Path = SOURCE_DIR, include_dir: Path = INCLUDE_DIR) -> str:
+    """16 hex digits of a SHA-256 over the binding's source, the C ABI
+    header, its flags and the torch version it compiles against."""
+    import torch
+
+    digest = hashlib.sha256()
+    fields = [HOST_SOURCE.encode(), (Path(source_dir) / HOST_SOURCE).read_bytes(),
+              (Path(include_dir) / "nanokv.h").read_bytes(), "\0".join(HOST_FLAGS).encode(),
+              torch.__version__.encode(), str(torch._C._GLIBCXX_USE_CXX11_ABI).encode()]
+    for field in fields:
+        digest.update(len(field).to_bytes(8, "little"))
+        digest.update(field)
+    return digest.hexdigest()[:16]
+
+
+def host_build_command(output: Path, source_dir: Path = SOURCE_DIR,
+                       include_dir: Path = INCLUDE_DIR) -> list[str]:
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    compiler = shutil.which("g++") or "g++"
+    includes = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], str(include_dir)]
+    libraries = cpp_extension.library_paths()
+    return [
+        compiler, *HOST_FLAGS,
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        "-DTORCH_EXTENSION_NAME=_nkv_host", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f'-DNKV_HOST_BUILD_ID="{host_build_id(source_dir, include_dir)}"',
+        *(f"-I{path}" for path in includes),
+        str(Path(source_dir) / HOST_SOURCE), "-o", str(output),
+        *(f"-L{path}" for path in libraries), *(f"-Wl,-rpath,{path}" for path in libraries),
+        "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+    ]
+
+
+def build_host(*, verbose: bool = False, output: Path | None = None,
+               source_dir: Path | None = None, include_dir: Path | None = None) -> Path:
+    """Compile the host binding (always) and install it atomically at
+    ``output`` (default :func:`host_module_path`)."""
+    target = Path(output) if output is not None else host_module_path()
+    source_dir = Path(source_dir) if source_dir is not None else SOURCE_DIR
+    include_dir = Path(include_dir) if include_dir is not None else INCLUDE_DIR
+    with tempfile.TemporaryDirectory(prefix="nanokv-host-") as tmp:
+        staged_build = Path(tmp) / target.name
+        command = host_build_command(staged_build, source_dir, include_dir)
+        if verbose:
+            print(" ".join(command), flush=True)
+        result = subprocess.run(command, capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError(f"g++ failed ({result.returncode}) building {target.name}:\n"
+                               f"{(result.stdout + result.stderr).strip()}")
+        target.parent.mkdir(parents=True, exist_ok=True)
+        staged = target.with_name(target.name + ".tmp")
+        shutil.copyfile(staged_build, staged)
+        os.replace(staged, target)
+    return target
+
+
 if __name__ == "__main__":
     path = build(verbose="-v" in sys.argv)
     print(path)
+    print(build_host(verbose="-v" in sys.argv))

@@ -21,13 +21,12 @@ from nanokv import _lib
 from nanokv.paged_kv import ops
 from nanokv.paged_kv.base import (
     PagedKVAllocation,
-    check_gather_inputs,
-    check_store_inputs,
     validate_store_inputs,
 )
 
 _LOAD_LOCK = Lock()
 _READY = False
+_HOST = None  # the C++ host binding, set by the first load
 
 
 def hip_runtime_available() -> bool:
@@ -55,12 +54,13 @@ class HIPPagedKVBackend:
 
     @staticmethod
     def _load() -> None:
-        global _READY
+        global _READY, _HOST
         if _READY:
             return
         with _LOAD_LOCK:
             if not _READY:
                 _lib.load_library()
+                _HOST = _lib.load_host()
                 ops.register_ops()
                 _READY = True
 
@@ -97,12 +97,11 @@ class HIPPagedKVBackend:
         return allocation.owner.copy_slots_async(host_slots)
 
     # store and gather are called once per layer and, in the reference's SDPA
-    # decode loop, twice per request per layer (attention.py:284-300), so
-    # their host path is kept short: the reference validator's checks
-    # (check_*_inputs: same order and messages, no dimension record built),
-    # then the launch core, which checks only what the kernel adds.  On
-    # MI355X a HIP launch alone costs ~3 us of host time and a torch
-    # allocation ~1.5 us; the rest is Python.
+    # decode loop, twice per request per layer (attention.py:284-300).  On
+    # MI355X a HIP launch alone costs ~3 us of host time, so the call runs in
+    # the C++ host binding (csrc/nkv_host.cpp): the reference validator's
+    # checks, in its order and with its messages, the output allocation and
+    # the C-ABI launch, on the caller's current stream.
 
     def store(
         self,
@@ -112,12 +111,11 @@ class HIPPagedKVBackend:
         value_cache: torch.Tensor,
         slot_mapping: torch.Tensor,
     ) -> None:
-        check_store_inputs(key, value, key_cache, value_cache, slot_mapping)
-        if not key.is_cuda:
-            raise ValueError("HIP Paged KV Store requires ROCm device tensors")
         if not _READY:
             self._load()
-        ops.store_checked(key, value, key_cache, value_cache, slot_mapping)
+        index = key.get_device()
+        _HOST.store(key, value, key_cache, value_cache, slot_mapping,
+                    ops.stream_of(index) if index >= 0 else 0)
 
     def gather(
         self,
@@ -125,12 +123,11 @@ class HIPPagedKVBackend:
         block_table: torch.Tensor,
         sequence_length: int,
     ) -> torch.Tensor:
-        check_gather_inputs(cache, block_table, sequence_length)
-        if not cache.is_cuda:
-            raise ValueError("HIP Paged KV Gather requires ROCm device tensors")
         if not _READY:
             self._load()
-        return ops.gather_checked(cache, block_table, sequence_length)
+        index = cache.get_device()
+        return _HOST.gather(cache, block_table, sequence_length,
+                            ops.stream_of(index) if index >= 0 else 0)
 
     def gather_varlen(
         self,

@@ -155,7 +155,7 @@ def _require_store_rows(key, value, key_cache, value_cache, slot_mapping) -> Non
         raise RuntimeError("Paged KV HIP Store: slot_mapping must hold one slot per token")
 
 
-def _stream_of(index: int) -> int:
+def stream_of(index: int) -> int:
     """The current stream of GPU ``index`` as a hipStream_t integer."""
     if _RAW_STREAM is not None:
         return _RAW_STREAM(index)
@@ -194,7 +194,7 @@ def store_checked(key, value, key_cache, value_cache, slot_mapping) -> None:
     status = _lib.load_library().nkv_store(
         key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
         slot_mapping.data_ptr(), num_tokens, kstride[0], vstride[0], shape[1] * shape[2],
-        cshape[0] * cshape[1], code, _stream_of(key.get_device()),
+        cshape[0] * cshape[1], code, stream_of(key.get_device()),
     )
     if status:
         _lib.check(status, "nanovllm_paged_kv::store")
@@ -218,7 +218,7 @@ def gather_checked(cache, block_table, sequence_length: int) -> torch.Tensor:
     status = _lib.load_library().nkv_gather(
         cache.data_ptr(), block_table.data_ptr(), block_table.shape[0], sequence_length,
         block_size, heads * head_dim, num_blocks, code, out.data_ptr(),
-        _stream_of(cache.get_device()),
+        stream_of(cache.get_device()),
     )
     if status:
         _lib.check(status, "nanovllm_paged_kv::gather")
