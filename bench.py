@@ -1328,83 +1328,41 @@ REFERENCE_MATRIX = {  # bench_paged_kv.py's defaults in the reference
 }
 
 
-def measure_reference_matrix(device, backend, iterations: int | None = None) -> dict:
-    """The reference's store/gather microbenchmark matrix
-    (nanovllm/benchmark/paged_kv.py:163-197, 240-323 with bench_paged_kv.py's
-    defaults): per case, a cache of 64 blocks of 16 slots, K/V from N(0,1),
-    slots a random permutation of the cache with every 11th slot -1, a random
-    block table; a bit-exact gate against the torch restatement, then p50 of
-    per-call event timings back to back, for the hip backend and the torch
-    restatement.  Effective bytes are the reference's (payload x 4 for store,
-    x 2 for gather)."""
+def measure_reference_matrix(device, backend=None, iterations: int | None = None) -> dict:
+    """The reference's store/gather micro-benchmark matrix with its defaults
+    (bench_paged_kv.py:58-148), run by nanokv.microbench for the hip backend
+    and for the reference's torch ops: per case a cache of 64 blocks of 16
+    slots, K/V from N(0,1), slots a random permutation of the cache with
+    every 11th slot -1, a random block table; a bit-exact gate against the
+    reference's torch ops, then the p50 of per-call event timings.  Effective
+    bytes are the reference's (payload x 4 for store, x 2 for gather)."""
     import numpy as np
-    import torch
 
-    from nanokv.benchmark import effective_bytes, linear_percentile
+    from nanokv import microbench as mb
 
     m = REFERENCE_MATRIX
     iterations = iterations or m["iterations"]
-    ref = reference_backend()
-    dtypes = {"float16": torch.float16, "bfloat16": torch.bfloat16}
-    words = {torch.float16: torch.int16, torch.bfloat16: torch.int16}
-    records = []
-    for op in m["operations"]:
-        for dtype_name in m["dtypes"]:
-            dtype = dtypes[dtype_name]
-            for heads, dim in m["kv_shapes"]:
-                for tokens in m["tokens"]:
-                    g = torch.Generator(device=device).manual_seed(m["seed"])
-                    shape = (m["num_blocks"], m["block_size"], heads, dim)
-                    kc = torch.empty(shape, dtype=dtype, device=device).normal_(generator=g)
-                    vc = torch.empty_like(kc).normal_(generator=g)
-                    key = torch.randn((tokens, heads, dim), dtype=dtype, device=device, generator=g)
-                    value = torch.randn_like(key)
-                    capacity = m["num_blocks"] * m["block_size"]
-                    slots = torch.randperm(capacity, dtype=torch.int32, device=device,
-                                           generator=g)[:tokens].contiguous()
-                    slots[::11] = -1
-                    table = torch.randperm(m["num_blocks"], dtype=torch.int32, device=device,
-                                           generator=g)
-                    if op == "store":
-                        ek, ev = kc.clone(), vc.clone()
-                        ref.store(key, value, ek, ev, slots)
-                        backend.store(key, value, kc, vc, slots)
-                        torch.cuda.synchronize()
-                        exact = (torch.equal(kc.view(words[dtype]), ek.view(words[dtype]))
-                                 and torch.equal(vc.view(words[dtype]), ev.view(words[dtype])))
-                        calls = {"hip": lambda: backend.store(key, value, kc, vc, slots),
-                                 "torch_reference": lambda: ref.store(key, value, kc, vc, slots)}
-                    else:
-                        expect = ref.gather(kc, table, tokens)
-                        got = backend.gather(kc, table, tokens)
-                        torch.cuda.synchronize()
-                        exact = torch.equal(got.view(words[dtype]), expect.view(words[dtype]))
-                        calls = {"hip": lambda: backend.gather(kc, table, tokens),
-                                 "torch_reference": lambda: ref.gather(kc, table, tokens)}
-                    if not exact:
-                        raise AssertionError(f"hip {op} differs from the torch reference "
-                                             f"({dtype_name}, {heads}x{dim}, {tokens} tokens)")
-                    nbytes = effective_bytes(op, tokens, heads, dim, kc.element_size())
-                    record = {"operation": op, "dtype": dtype_name, "tokens": tokens,
-                              "kv_shape": f"{heads}x{dim}", "effective_bytes": nbytes}
-                    for name, call in calls.items():
-                        for _ in range(m["warmup"]):
-                            call()
-                        torch.cuda.synchronize()
-                        pairs = [(torch.cuda.Event(enable_timing=True),
-                                  torch.cuda.Event(enable_timing=True)) for _ in range(iterations)]
-                        for start, end in pairs:
-                            start.record()
-                            call()
-                            end.record()
-                        pairs[-1][1].synchronize()
-                        p50 = linear_percentile([a.elapsed_time(b) * 1e3 for a, b in pairs], 0.5)
-                        record[f"{name}_p50_us"] = round(p50, 3)
-                        record[f"{name}_gbps"] = round(nbytes / (p50 * 1e3), 3)
-                    records.append(record)
+    cases = mb.expand_matrix(backends=("hip", "pytorch"), operations=m["operations"],
+                             dtypes=tuple(mb.DTYPES[n] for n in m["dtypes"]),
+                             token_counts=m["tokens"], kv_shapes=m["kv_shapes"],
+                             block_size=m["block_size"], num_blocks=m["num_blocks"],
+                             mapping=m["mapping"], seed=m["seed"])
+    by_case: dict[str, dict] = {}
+    for case in cases:
+        result = mb.run_case(case, warmup=m["warmup"], iterations=iterations, device=device)
+        key = case.selector.split(";", 1)[1]  # the selector without its backend
+        record = by_case.setdefault(key, {
+            "operation": case.operation, "dtype": mb.DTYPE_NAMES[case.dtype],
+            "tokens": case.num_tokens, "kv_shape": f"{case.num_kv_heads}x{case.head_dim}",
+            "effective_bytes": result["effective_bytes"]})
+        name = "hip" if case.backend == "hip" else "torch_reference"
+        record[f"{name}_p50_us"] = round(result["latency"]["p50_us"], 3)
+        record[f"{name}_gbps"] = round(result["effective_gbps_at_p50"], 3)
+    records = list(by_case.values())
     ratios = [r["torch_reference_p50_us"] / r["hip_p50_us"] for r in records]
     return {"cases": records, "geomean_speedup_of_hip": round(float(np.exp(np.mean(np.log(ratios)))), 3),
-            "iterations": iterations, "warmup": m["warmup"]}
+            "iterations": iterations, "warmup": m["warmup"], "runner": "nanokv.microbench",
+            "schema_of_full_reports": mb.SCHEMA}
 
 
 def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer,
