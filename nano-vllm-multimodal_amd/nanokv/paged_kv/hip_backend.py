@@ -35,9 +35,10 @@ def hip_runtime_available() -> bool:
 
 
 def hip_extension_available() -> bool:
-    """True when the built library loads and exports the full ABI."""
+    """True when the built library and its host binding load, export the
+    full ABI and match the sources (their build ids)."""
     try:
-        _lib.load_library()
+        _lib.load_host()
     except RuntimeError:
         return False
     return True
