@@ -797,12 +797,9 @@ def check_decode_attention(backend, case: dict, sample: int = 6) -> None:
 
 def decode_kernel_name(kv_heads: int, group: int) -> str:
     """The kernel nkv_paged_attention_decode runs for a head layout: the
-    MFMA kernel, or the VALU kernel for 1-2 query heads per kv head over 1,
-    2, 4 or 8 kv heads when NKV_DECODE_VALU=1 is set."""
-    import os
-
-    valu = os.environ.get("NKV_DECODE_VALU") == "1" and group <= 2 and kv_heads in (1, 2, 4, 8)
-    return "attn_decode_partial_kernel" if valu else "attn_decode_mfma_kernel"
+    range split below 8 kv heads, the entry split from 8 on (any group of
+    up to 16 query heads per kv head)."""
+    return "attn_decode_entry_kernel" if kv_heads >= 8 else "attn_decode_range_kernel"
 
 
 def measure_grouped_decode(device, backend, wl, reps: int) -> list[dict]:

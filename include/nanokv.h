@@ -341,11 +341,8 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  * with a result in the input type; scale must be finite and positive
  * (NKV_E_INVALID otherwise).  An empty context yields zeros.  dtype
  * NKV_DTYPE_BFLOAT16 or NKV_DTYPE_FLOAT16 (q, caches and out alike),
- * head_dim 128, any num_kv_heads, G <= 16.  Every layout runs on the MFMA
- * kernel, which rounds the softmax weights to the input type before the
- * product with V, as flash attention does.  With NKV_DECODE_VALU=1 in the
- * environment (read on every call), G = 1 or 2 with 1, 2, 4 or 8 kv heads
- * runs on the VALU kernel instead, which keeps the weights in fp32.
+ * head_dim 128, any num_kv_heads, G <= 16.  The weights are rounded to the
+ * input type before the product with V, as flash attention does.
  *
  * Replaces: the decode call flash_attn_with_kvcache(q, k_cache, v_cache,
  *   cache_seqlens=context_lens, block_table=block_tables, softmax_scale,
@@ -353,21 +350,31 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  *   122-130); numerically the decode branch of SDPAAttention
  *   (attention.py:284-300: per-request gather, then SDPA with GQA).
  *
- * nkv_build_attention_plan cuts every context into entries of
- *   nkv_attention_entry_rows(block_size) rows (whole blocks, 768 rows by
- *   default) and writes one int4 {row0, rows, seq, 0} per entry into `plan`
- *   (capacity >= nkv_attention_plan_capacity(total context tokens,
- *   num_seqs, block_size)) and each sequence's first entry into first_part
- *   [num_seqs+1].  It reads only cu_seqlens_k, so one plan serves every
- *   layer of a step and stays valid while the context lengths do.
- * nkv_paged_attention_decode runs the split-K partial kernel and the
- *   merge; block_tables [num_seqs, table_stride] (int32, -1 padded) map
- *   context rows to cache blocks, a block id outside [0, num_blocks) or a
- *   row past the table drops its rows; workspace holds
- *   nkv_attention_workspace_bytes(capacity, num_q_heads, head_dim) bytes
- *   (16-byte aligned).  q is [num_seqs, num_q_heads, head_dim] with row
- *   stride q_seq_stride elements; out is [num_seqs, num_q_heads, head_dim]
- *   with row stride out_seq_stride (even).
+ * nkv_build_attention_plan splits the contexts for the decode kernels and
+ *   writes the split into `plan` (capacity >= nkv_attention_plan_capacity(
+ *   total context tokens, num_seqs, block_size) int4 entries, 16-byte
+ *   aligned) and each sequence's first partial into first_part
+ *   [num_seqs+1].  Below 8 kv heads (the range split) it lays the contexts
+ *   end to end in 16-row chunks and cuts them into equal contiguous ranges,
+ *   one per worker (1024 / num_kv_heads per kv head, so that a launch is
+ *   one wavefront per SIMD of MI355X; a range crosses sequence
+ *   boundaries); from 8 kv heads on (the entry split) it cuts every context
+ *   into entries of nkv_attention_entry_rows(block_size) rows (whole
+ *   blocks, 768 rows by default), one int4 {row0, rows, seq, 0} each.  It
+ *   reads only cu_seqlens_k, so one plan serves every layer of a step; it
+ *   is valid for those context lengths and that kv-head count only (a
+ *   range plan used with another batch size or kv-head count makes the
+ *   decode write nothing; a plan for other lengths of the same batch
+ *   computes over the wrong rows).
+ * nkv_paged_attention_decode runs the split-K partial kernel (one
+ *   wavefront per worker and kv head, or one workgroup per entry and kv
+ *   head) and the merge; block_tables
+ *   [num_seqs, table_stride] (int32, -1 padded) map context rows to cache
+ *   blocks, a block id outside [0, num_blocks) or a row past the table
+ *   drops its rows; workspace holds nkv_attention_workspace_bytes(capacity,
+ *   num_q_heads, head_dim) bytes (16-byte aligned).  q is [num_seqs,
+ *   num_q_heads, head_dim] with row stride q_seq_stride elements; out is
+ *   [num_seqs, num_q_heads, head_dim] with row stride out_seq_stride (even).
  */
 int64_t nkv_attention_entry_rows(int64_t block_size);
 int64_t nkv_attention_plan_capacity(int64_t total_tokens, int64_t num_seqs,
@@ -375,7 +382,8 @@ int64_t nkv_attention_plan_capacity(int64_t total_tokens, int64_t num_seqs,
 int64_t nkv_attention_workspace_bytes(int64_t capacity, int64_t num_q_heads,
                                       int64_t head_dim);
 int nkv_build_attention_plan(const int32_t* cu_seqlens_k, int64_t num_seqs,
-                             int64_t block_size, void* plan, int64_t capacity,
+                             int64_t block_size, int64_t num_kv_heads,
+                             void* plan, int64_t capacity,
                              int32_t* first_part, void* stream);
 int nkv_paged_attention_decode(const void* q, int64_t q_seq_stride,
                                const void* key_cache, const void* value_cache,

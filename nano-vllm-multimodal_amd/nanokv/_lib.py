@@ -109,7 +109,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     "nkv_attention_workspace_bytes": (c_i64, (c_i64, c_i64, c_i64)),
     "nkv_build_attention_plan": (
         ctypes.c_int,
-        (c_ptr, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr),
+        (c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr, c_ptr),
     ),
     "nkv_paged_attention_decode": (
         ctypes.c_int,

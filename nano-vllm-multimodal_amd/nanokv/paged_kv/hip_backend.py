@@ -44,6 +44,20 @@ def hip_extension_available() -> bool:
     return True
 
 
+class AttentionPlan(tuple):
+    """``(plan, first_part)`` of :meth:`HIPPagedKVBackend.build_attention_plan`,
+    unpacked like the pair, with ``lengths`` = (total context rows, number
+    of sequences, kv heads) it was built for: a plan splits those rows among
+    the kernel's workers of each kv head, so it serves only contexts of the
+    same lengths in caches with as many kv heads."""
+
+    def __new__(cls, plan: torch.Tensor, first_part: torch.Tensor,
+                lengths: tuple[int, int, int]):
+        self = super().__new__(cls, (plan, first_part))
+        self.lengths = lengths
+        return self
+
+
 def reset_hip_backend_state_for_tests() -> None:
     global _READY
     with _LOAD_LOCK:
@@ -260,15 +274,18 @@ class HIPPagedKVBackend:
         cache: torch.Tensor,
         cu_seqlens_k: torch.Tensor,
         total_tokens: int,
-    ) -> tuple[torch.Tensor, torch.Tensor]:
-        """(plan, first_part) for :meth:`paged_attention_decode`: each
-        context cut into entries of whole blocks (768 rows by default).  It
-        depends on the context lengths only, so one plan serves every layer
-        of a step (and every step with the same lengths)."""
+    ) -> "AttentionPlan":
+        """(plan, first_part) for :meth:`paged_attention_decode`: the
+        contexts, in 16-row chunks laid end to end, split into equal ranges,
+        one per worker wavefront of the kernel (1024 / Hkv per kv head of
+        ``cache``).  It depends on the context lengths and the kv-head count
+        only, so one plan serves every layer of a step (and every step with
+        the same lengths)."""
         self._load()
-        return ops.build_attention_plan(
-            cu_seqlens_k, total_tokens, cache.shape[1]
-        )
+        plan, first_part = ops.build_attention_plan(cu_seqlens_k, total_tokens, cache.shape[1],
+                                                    cache.shape[2])
+        return AttentionPlan(plan, first_part,
+                             (int(total_tokens), int(cu_seqlens_k.numel()) - 1, int(cache.shape[2])))
 
     def paged_attention_decode(
         self,
@@ -300,12 +317,19 @@ class HIPPagedKVBackend:
         if plan is None:
             plan = self.build_attention_plan(key_cache, cu_seqlens_k, total_tokens)
         else:
+            built_for = getattr(plan, "lengths", None)
+            here = (int(total_tokens), block_tables.shape[0], key_cache.shape[2])
+            if built_for is not None and built_for != here:
+                raise ValueError(f"attention plan was built for {built_for[0]} context rows over "
+                                 f"{built_for[1]} sequences and {built_for[2]} kv heads, not "
+                                 f"{here[0]} over {here[1]} and {here[2]}: build it with "
+                                 "build_attention_plan for these lengths and this cache")
             need = int(_lib.load_library().nkv_attention_plan_capacity(
                 total_tokens, block_tables.shape[0], key_cache.shape[1]))
             if plan[0].shape[0] < need:
-                raise ValueError(f"attention plan has {plan[0].shape[0]} entries, {total_tokens} "
-                                 f"context rows need {need}: build it with build_attention_plan "
-                                 "for the same lengths and block size")
+                raise ValueError(f"attention plan has {plan[0].shape[0]} entries, "
+                                 f"{block_tables.shape[0]} sequences need {need}: build it with "
+                                 "build_attention_plan for these lengths")
         if out is None:
             out = torch.empty_like(q)
         ops.paged_attention_decode(

@@ -21,7 +21,7 @@ too, paged_kv_cuda.cu:168-171).  Additive ops, with no reference schema:
     gather_varlen_planned(Tensor key_cache, Tensor value_cache, Tensor plan,
                           Tensor(a!) key_out, Tensor(b!) value_out) -> ()
     build_attention_plan(Tensor cu_seqlens_k, int total_tokens,
-                         int block_size) -> (Tensor, Tensor)
+                         int block_size, int num_kv_heads) -> (Tensor, Tensor)
     paged_attention_decode(Tensor q, Tensor key_cache, Tensor value_cache,
                            Tensor block_tables, Tensor plan,
                            Tensor first_part, float scale,
@@ -59,7 +59,7 @@ SCHEMAS = {
     "gather_varlen_planned": "gather_varlen_planned(Tensor key_cache, Tensor value_cache, "
     "Tensor plan, Tensor(a!) key_out, Tensor(b!) value_out) -> ()",
     "build_attention_plan": "build_attention_plan(Tensor cu_seqlens_k, int total_tokens, "
-    "int block_size) -> (Tensor, Tensor)",
+    "int block_size, int num_kv_heads) -> (Tensor, Tensor)",
     "paged_attention_decode": "paged_attention_decode(Tensor q, Tensor key_cache, "
     "Tensor value_cache, Tensor block_tables, Tensor plan, Tensor first_part, float scale, "
     "Tensor(a!) out) -> ()",
@@ -394,7 +394,8 @@ def _store_gather_impl(key, value, key_cache, value_cache, slot_mapping, plan, n
     _lib.check(status, "nanovllm_paged_kv::store_gather")
 
 
-def _build_attention_plan_impl(cu_seqlens_k, total_tokens: int, block_size: int):
+def _build_attention_plan_impl(cu_seqlens_k, total_tokens: int, block_size: int,
+                               num_kv_heads: int):
     device = _require_device("paged KV HIP attention plan", cu_seqlens_k)
     if cu_seqlens_k.dtype != torch.int32 or cu_seqlens_k.ndim != 1 or not cu_seqlens_k.is_contiguous():
         raise ValueError("cu_seqlens_k must be a contiguous 1-D int32 tensor")
@@ -407,6 +408,7 @@ def _build_attention_plan_impl(cu_seqlens_k, total_tokens: int, block_size: int)
         cu_seqlens_k.data_ptr(),
         num_seqs,
         block_size,
+        num_kv_heads,
         plan.data_ptr() if capacity else None,
         capacity,
         first_part.data_ptr(),

@@ -514,14 +514,15 @@ def algorithmic_bytes_for(case: str) -> dict[str, int]:
         total = int(wl.num_tokens.sum())
         q_bytes = wl.num_seqs * 16 * wl.head_dim * 2
         nbytes = total * wl.row_bytes * 2 + 2 * q_bytes
-        # the MFMA kernel by default, the VALU kernel under NKV_DECODE_VALU=1
-        return {"attn_decode_mfma_kernel": nbytes, "attn_decode_partial_kernel": nbytes}
+        # the entry split at 8 kv heads, the range split below
+        return {"attn_decode_entry_kernel": nbytes, "attn_decode_range_kernel": nbytes}
     if case in GROUPED:
         hkv, group = GROUPED[case]
         wl = workloads.build("decode_step", num_layers=1)
         total = int(wl.num_tokens.sum())
         q_bytes = wl.num_seqs * hkv * group * 128 * 2
-        return {"attn_decode_mfma_kernel": total * hkv * 128 * 2 * 2 + 2 * q_bytes}
+        nbytes = total * hkv * 128 * 2 * 2 + 2 * q_bytes
+        return {"attn_decode_entry_kernel": nbytes, "attn_decode_range_kernel": nbytes}
     if case in ("prefill_attention", "block_pool"):
         return {}
     if case == "store_floor":

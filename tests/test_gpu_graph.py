@@ -127,25 +127,18 @@ def test_captured_decode_graph_replays_match_oracle(gpu_device):
     del plan_keepalive
 
 
-@pytest.mark.parametrize("kernel,kv_heads,q_heads", [("mfma", 8, 16), ("valu", 8, 16),
-                                                     ("mfma", 2, 16)])
-def test_captured_flash_decode_replays_match_oracle(gpu_device, monkeypatch, kernel, kv_heads,
-                                                    q_heads):
+@pytest.mark.parametrize("kv_heads,q_heads", [(8, 16), (2, 16)])
+def test_captured_flash_decode_replays_match_oracle(gpu_device, kv_heads, q_heads):
     """The reference's graph decode on the Flash path (model_runner.py:
     1079-1157 captures Attention.forward; attention.py:87-93 store,
     :122-130 flash_attn_with_kvcache), with the drop-in from nanokv.flash:
     per layer, store then decode attention over the paged cache, captured
     once and replayed for batches of 1..bucket sequences (padding rows have
-    context length 0).  The MFMA kernel serves every layout; "valu" captures
-    16 query heads over 8 kv heads on the VALU kernel (NKV_DECODE_VALU=1,
-    read when the call is captured).  Every replay's cache is checked bit
-    for bit and its attention output within 1e-3 + 2^-8 (ref_abs + |ref|)
-    against the oracle (ref_abs: the same attention over |V|; the MFMA
+    context length 0; the attention plan is built inside the graph, so
+    each replay splits its own lengths).  Every replay's cache is checked
+    bit for bit and its attention output within 1e-3 + 2^-8 (ref_abs +
+    |ref|) against the oracle (ref_abs: the same attention over |V|; the
     kernel rounds its weights to bf16)."""
-    if kernel == "valu":
-        monkeypatch.setenv("NKV_DECODE_VALU", "1")
-    else:
-        monkeypatch.delenv("NKV_DECODE_VALU", raising=False)
     from nanokv.flash import flash_attn_with_kvcache
     from nanokv.packing import DecodeGraphBuffers, DevicePacker, SequenceBatch
     from nanokv.paged_kv import create_paged_kv_backend

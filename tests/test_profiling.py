@@ -55,8 +55,8 @@ def write_counters(path, rows):
     (STORE, "store_rows_kernel<16>"),
     (GATHER, "gather_planned_kernel<16, false>"),
     (COPY, "__amd_rocclr_copyBuffer"),
-    ("void nkv::(anonymous namespace)::attn_decode_partial_kernel<8, 2, false>(int)",
-     "attn_decode_partial_kernel<8, 2, false>"),
+    ("void nkv::(anonymous namespace)::attn_decode_range_kernel<false, true>(int)",
+     "attn_decode_range_kernel<false, true>"),
     ("void at::native::reduce_kernel<512, 1, at::native::ReduceOp<long, at::native::func_wrapper_t"
      "<long, at::native::sum_functor<long, long, long>::operator()(at::TensorIterator&)::{lambda(long,"
      " long)#1}>, unsigned int, long, 4, 4> >(at::native::ReduceOp<long>)", None),
@@ -169,8 +169,9 @@ def test_prefill_flops_match_the_bench_workload():
     from nanokv import workloads
 
     total = int(workloads.build("decode_step", num_layers=1).num_tokens.sum())
+    nbytes = total * 2 * 128 * 2 * 2 + 2 * 256 * 16 * 128 * 2
     assert profiling.algorithmic_bytes_for("grouped_decode_2x8") == {
-        "attn_decode_mfma_kernel": total * 2 * 128 * 2 * 2 + 2 * 256 * 16 * 128 * 2}
+        "attn_decode_entry_kernel": nbytes, "attn_decode_range_kernel": nbytes}
 
 
 FAKE_ROCPROF = '''#!{python}
