@@ -127,7 +127,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens=None, block_table
     capturing = torch.cuda.is_current_stream_capturing()
     version = None if cache_seqlens.is_inference() else cache_seqlens._version
     key = (cache_seqlens.data_ptr(), version, tuple(cache_seqlens.shape), str(q.device),
-           int(k_cache.shape[1]))
+           int(k_cache.shape[1]), int(k_cache.shape[2]))
     cache_ptr = k_cache.data_ptr()
     cached = None if capturing else _STEP_PLAN.lookup(cache_seqlens, key, cache_ptr)
     if cached is not None:

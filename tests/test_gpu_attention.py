@@ -435,11 +435,12 @@ def test_rows_outside_the_contexts_may_hold_any_bits(backend, gpu_device, hkv,
     check_close(out, reference(host, scale), f"any-bits rows hkv={hkv} g={g}")
 
 
-@pytest.mark.parametrize("hkv,g", [(8, 2), (8, 4)])
+@pytest.mark.parametrize("hkv,g", [(8, 2), (8, 4), (2, 8), (4, 4)])
 def test_cache_over_4gib(backend, gpu_device, hkv, g):
     """Caches larger than 4 GiB, whose row byte offsets need more than 32
-    bits (the kernel's 64-bit-address instance): the contexts' blocks are
-    moved to the top of each cache."""
+    bits (the 64-bit-address instances of the entry kernel, 8 kv heads, and
+    of the range kernel, 2 and 4): the contexts' blocks are moved to the
+    top of each cache."""
     bs = 256
     lens = [300, 700, 1, 513]
     dev, host, total = build_case(gpu_device, hkv, g, bs, lens, seed=43)

@@ -409,7 +409,8 @@ def test_flash_with_kvcache_matches_decode_oracle(gpu_device, dtype):
     check_decode(out, host, k_lens, 0.088, "flash_attn_with_kvcache")
 
 
-def test_flash_with_kvcache_plan_follows_each_step(gpu_device):
+@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
+def test_flash_with_kvcache_plan_follows_each_step(gpu_device, hkv, g):
     """The decode drop-in builds one plan per step (on its first call, after
     one read of the context total) and reuses it for the step's other
     layers, which pass the same lengths tensor and caches of their own.  It
@@ -417,13 +418,14 @@ def test_flash_with_kvcache_plan_follows_each_step(gpu_device):
     the tensor's version), a new batch packed into the same graph buffers by
     the device packer (which bumps the versions of what its kernel wrote),
     and a layer's cache coming back (the next step).  The longer contexts
-    come second, so a stale plan would drop rows and miss the oracle."""
+    come second, so a stale plan would drop rows and miss the oracle; both
+    splits (8 kv heads: entries, 2: ranges)."""
     from nanokv import flash
     from nanokv.packing import DecodeGraphBuffers, DevicePacker, SequenceBatch
 
     bs = 16
     long_lens = [1, 300, 17, 64]
-    dev, host = build_case(gpu_device, 8, 2, bs, [1] * 4, long_lens, seed=53)
+    dev, host = build_case(gpu_device, hkv, g, bs, [1] * 4, long_lens, seed=53)
     q = dev["q"].unsqueeze(1)
     # three "layers": the same cache contents at three addresses
     layers = [(dev["kc"], dev["vc"])] + [(dev["kc"].clone(), dev["vc"].clone()) for _ in range(2)]
