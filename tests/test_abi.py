@@ -82,6 +82,11 @@ def test_version_and_plan_geometry():
                                             256, 16, -0.5, 1, None, 0, None, 2048, None), "positive"),
     (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 8, 16, 128,
                                             256, 16, float("nan"), 1, None, 0, None, 2048, None), "finite"),
+    # the range split (fewer than 8 kv heads) needs its whole plan
+    (lambda l: l.nkv_paged_attention_decode(None, 2048, None, None, None, 4, None, 4, None, 1, 2, 16, 128,
+                                            256, 16, 0.1, 1, None, 0, None, 2048, None), "plan capacity"),
+    (lambda l: l.nkv_build_attention_plan(None, 1, 256, 2, None, 4, None, None), "capacity 4"),
+    (lambda l: l.nkv_build_attention_plan(None, 1, 256, 0, None, 4096, None, None), "num_kv_heads"),
     (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 5000, 8, 40, 16, 8, 10, 1, None, 144,
                                              None), "num_seqs"),
     (lambda l: l.nkv_build_store_gather_plan(None, 4, None, None, 2, 8, 40, 16, 8, 10, 1, None, 16,
