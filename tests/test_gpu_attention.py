@@ -289,6 +289,33 @@ def test_long_contexts_over_small_blocks(backend, gpu_device, hkv, g, bs):
     check_close(out, ref, f"hkv={hkv} g={g} bs={bs}")
 
 
+@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8), (1, 1), (4, 16)])
+@pytest.mark.parametrize("lens", [[0], [0, 0, 0], [1], [1, 1, 1], [0, 1, 0], [16], [17, 0]])
+def test_empty_and_tiny_batches(backend, gpu_device, hkv, g, lens):
+    """Every context empty (the range split has no units and no workers;
+    each output row must be zeros), and one-token or one-chunk contexts
+    (worker ranges of a start-up unit and at most two chunks)."""
+    dev, host, total = build_case(gpu_device, hkv, g, 16, lens, seed=31 + sum(lens))
+    out = torch.full_like(dev["q"], float("nan"))
+    backend.paged_attention_decode(dev["q"], dev["kc"], dev["vc"], dev["tables"], dev["cu"],
+                                   total, 0.1, out=out)
+    check_close(out, reference(host, 0.1), f"hkv={hkv} g={g} lens={lens}")
+    for i, n in enumerate(lens):
+        if n == 0:
+            assert torch.all(out[i] == 0), f"empty context {i} must give zeros"
+
+
+@pytest.mark.parametrize("hkv,g", [(8, 2), (2, 8)])
+def test_no_sequences(backend, gpu_device, hkv, g):
+    """A batch of no sequences: an empty output, no launch reads a plan."""
+    kc = torch.zeros((4, 16, hkv, 128), dtype=torch.bfloat16, device=gpu_device)
+    tables = torch.zeros((0, 1), dtype=torch.int32, device=gpu_device)
+    cu = torch.zeros(1, dtype=torch.int32, device=gpu_device)
+    q = torch.zeros((0, hkv * g, 128), dtype=torch.bfloat16, device=gpu_device)
+    out = backend.paged_attention_decode(q, kc, kc, tables, cu, 0, 0.1)
+    assert out.shape == (0, hkv * g, 128)
+
+
 def test_plan_at_the_sequence_limit(backend, gpu_device):
     """NKV_MAX_PLAN_SEQS (8192) sequences, lengths 0 .. 3000: the plan
     kernel's LDS scan at its largest; the whole plan equals the
