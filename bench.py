@@ -113,6 +113,9 @@ def parse_args(argv=None):
                         "ops (0 disables the CPU leg)")
     p.add_argument("--cpu-baseline-repeats", type=int, default=3,
                    help="runs of the 28-layer step in the OpenMP port's figure")
+    p.add_argument("--cpu-baseline-runs", type=int, default=5,
+                   help="runs of the sampled decode step through the reference's torch ops; "
+                        "the median run is reported (about 2 s each on 16 cores)")
     p.add_argument("--workload-iterations", type=int, default=30,
                    help="timed launches per operation of the single-layer configurations; 0 = skip")
     p.add_argument("--no-gpu-reference", dest="gpu_reference", action="store_false",
@@ -600,7 +603,8 @@ def main(argv=None) -> int:
 
         cpu_baseline = cpu_baseline_leg(wl, args.cpu_baseline_layers, args.cpu_baseline_repeats,
                                         check_layers, gpu_layer,
-                                        args.cpu_baseline_workloads.split(","))
+                                        args.cpu_baseline_workloads.split(","),
+                                        runs=args.cpu_baseline_runs)
 
     result = {
         "metric": METRIC,
@@ -1363,7 +1367,7 @@ def measure_reference_matrix(device, backend=None, iterations: int | None = None
 
 
 def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer,
-                     workload_names) -> dict:
+                     workload_names, runs: int = 5) -> dict:
     """The CPU leg: the oracle checks the GPU's outputs of ``check_layers``
     (store+gather bit-exact; attention within attention_tolerance of the fp32
     oracle on 32 sequences); then the reference pytorch backend's torch ops
@@ -1406,7 +1410,7 @@ def cpu_baseline_leg(wl, layers: int, repeats: int, check_layers, gpu_layer,
                                  f"(max err {err.max():.3e})")
         log(f"[bench] layer {layer}: store+gather bit-exact, attention max err {err.max():.2e} vs oracle")
         checked.append(layer)
-    result = cpu_reference_baseline(wl, layers, workload_names)
+    result = cpu_reference_baseline(wl, layers, workload_names, runs=runs)
     result["checked_layers"] = checked
     result["openmp_port"] = openmp_port_baseline(wl, wl.num_layers, repeats)
 
@@ -1461,7 +1465,7 @@ def _median_seconds(fn, *, min_runs: int = 3, budget_s: float = 2.0) -> tuple[fl
     return times[len(times) // 2], len(times)
 
 
-def cpu_reference_baseline(wl, layers: int, workload_names) -> dict:
+def cpu_reference_baseline(wl, layers: int, workload_names, runs: int = 5) -> dict:
     """The reference's own CPU path: the ``pytorch`` backend's torch ops
     (index_copy_ store, index_select gather of whole blocks,
     nanovllm/layers/paged_kv/pytorch_backend.py:26-50, with the validators
@@ -1472,8 +1476,8 @@ def cpu_reference_baseline(wl, layers: int, workload_names) -> dict:
 
     The decode step is sampled: ``layers`` layers (each with its own new
     rows) against ONE layer-sized host cache (the 28-layer cache does not fit
-    host memory), bytes counted as on the GPU; the per-layer time scales to
-    the 28-layer step.  The single-layer configurations are timed whole, each
+    host memory), bytes counted as on the GPU, run ``runs`` times; the median
+    run's per-layer time scales to the 28-layer step.  The single-layer configurations are timed whole, each
     operation as the median of at least 3 runs."""
     import numpy as np
     import torch
@@ -1499,10 +1503,13 @@ def cpu_reference_baseline(wl, layers: int, workload_names) -> dict:
                 ref.gather(vc, tables[i], n)
 
         layer(0)
-        t0 = time.perf_counter()
-        for index in range(layers):
-            layer(index % wl.num_layers)
-        per_layer = (time.perf_counter() - t0) / layers
+        run_s = []
+        for _ in range(max(1, runs)):
+            t0 = time.perf_counter()
+            for index in range(layers):
+                layer(index % wl.num_layers)
+            run_s.append((time.perf_counter() - t0) / layers)
+        per_layer = sorted(run_s)[len(run_s) // 2]
         layer_bytes = wl.store_bytes(layers=1) + wl.gather_bytes(layers=1)
         del kc, vc
         configs = {}
@@ -1544,9 +1551,11 @@ def cpu_reference_baseline(wl, layers: int, workload_names) -> dict:
                "index_select gather) on host tensors; a port of the reference's Python code, which "
                "is read here, not imported",
         "sample": (f"decode step: {layers} of the 28 layers (store of the 256 new rows, then 256 x 2 "
-                   f"per-sequence gathers of K and V) on host tensors, one layer-sized cache, "
-                   f"{per_layer:.2f} s per layer"),
+                   f"per-sequence gathers of K and V) on host tensors, one layer-sized cache; "
+                   f"median of {len(run_s)} runs ({layers * sum(run_s):.1f} s of CPU work), "
+                   f"{per_layer:.3f} s per layer (runs {min(run_s):.3f}-{max(run_s):.3f})"),
         "seconds_per_layer": round(per_layer, 4),
+        "seconds_per_layer_runs": [round(x, 4) for x in run_s],
         "decode_tokens_per_s_equivalent": round(wl.num_seqs / (per_layer * wl.num_layers), 3),
         "torch_threads": threads,
         "cpu_model": cpu_model(),

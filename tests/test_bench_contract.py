@@ -46,8 +46,11 @@ def test_cpu_baselines_run_on_a_small_step():
     import bench
 
     wl = workloads.build("decode_step", num_layers=2, num_live=8, churn=2, max_ctx=1024)
-    result = bench.cpu_reference_baseline(wl, 2, [])
+    result = bench.cpu_reference_baseline(wl, 2, [], runs=3)
     assert result["kind"] == "port" and result["unit"] == "GB/s"
+    runs = result["seconds_per_layer_runs"]
+    assert len(runs) == 3 and result["seconds_per_layer"] == sorted(runs)[1]
+    assert "median of 3 runs" in result["sample"]
     assert result["value"] > 0 and result["cores"] >= 1 and result["torch_threads"] == result["cores"]
     assert "index_copy_" in result["ops"] and result["cpu_model"]
     port = bench.openmp_port_baseline(wl, layers=2, repeats=1)
