@@ -363,9 +363,9 @@ int nkv_pack_prefill(const int32_t* num_cached, const int32_t* num_scheduled,
  *   blocks, 768 rows by default), one int4 {row0, rows, seq, 0} each.  It
  *   reads only cu_seqlens_k, so one plan serves every layer of a step; it
  *   is valid for those context lengths and that kv-head count only (a
- *   range plan used with another batch size or kv-head count makes the
- *   decode write nothing; a plan for other lengths of the same batch
- *   computes over the wrong rows).
+ *   range plan used with another batch size or kv-head count computes no
+ *   partial, and the merge writes NaN to every output; a plan for other
+ *   lengths of the same batch computes over the wrong rows).
  * nkv_paged_attention_decode runs the split-K partial kernel (one
  *   wavefront per worker and kv head, or one workgroup per entry and kv
  *   head) and the merge; block_tables

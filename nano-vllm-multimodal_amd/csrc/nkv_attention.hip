@@ -1112,14 +1112,27 @@ constexpr int kReduceBatch = 8;  // parts in flight per lane
 template <bool kHalf>
 __global__ __launch_bounds__(kReduceThreads) void attn_decode_reduce_kernel(
     const uint32_t* __restrict__ part_acc, const f32x2* __restrict__ part_ml,
-    const int32_t* __restrict__ first_part, int64_t capacity, int32_t num_seqs,
-    int32_t num_q_heads, uint16_t* __restrict__ out, int64_t out_seq_stride) {
+    const int32_t* __restrict__ first_part, const int4* __restrict__ range_plan,
+    int32_t num_kv_heads, int64_t capacity, int32_t num_seqs, int32_t num_q_heads,
+    uint16_t* __restrict__ out, int64_t out_seq_stride) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t pair = static_cast<int64_t>(blockIdx.x) * kReduceWaves + wave;
   if (pair >= static_cast<int64_t>(num_seqs) * num_q_heads) return;  // whole waves; no barrier
   const int32_t seq = static_cast<int32_t>(pair / num_q_heads);
   const int32_t qh = static_cast<int32_t>(pair % num_q_heads);
+  uint16_t* const dst = out + static_cast<int64_t>(seq) * out_seq_stride + qh * kHeadDim + 2 * lane;
+  // A range plan built for another sequence or kv-head count: the range
+  // kernel wrote no partial, so the workspace holds stale values.  Every
+  // output becomes NaN instead.
+  if (range_plan != nullptr) {
+    const const_i32* const header = (const const_i32*)range_plan;
+    if (header[2] != num_seqs || header[3] != num_kv_heads) {
+      const uint16_t nan = kHalf ? 0x7E00u : 0x7FC0u;
+      *reinterpret_cast<uint32_t*>(dst) = static_cast<uint32_t>(nan) | (static_cast<uint32_t>(nan) << 16);
+      return;
+    }
+  }
   const int64_t p0 = max(0, first_part[seq]);
   const int64_t p1 = min(capacity, static_cast<int64_t>(first_part[seq + 1]));
 
@@ -1159,8 +1172,7 @@ __global__ __launch_bounds__(kReduceThreads) void attn_decode_reduce_kernel(
   const bool any = lsum > 0.f;
   const uint32_t packed = static_cast<uint32_t>(from_f32<kHalf>(any ? ax / lsum : 0.f)) |
                           (static_cast<uint32_t>(from_f32<kHalf>(any ? ay / lsum : 0.f)) << 16);
-  *reinterpret_cast<uint32_t*>(out + static_cast<int64_t>(seq) * out_seq_stride +
-                               qh * kHeadDim + 2 * lane) = packed;
+  *reinterpret_cast<uint32_t*>(dst) = packed;
 }
 
 using RangeKernel = void (*)(const uint16_t*, int64_t, const uint8_t*, const uint8_t*,
@@ -1352,15 +1364,18 @@ extern "C" int nkv_paged_attention_decode(
   if (int rc = nkv_check_launch("nkv_paged_attention_decode (partials)")) return rc;
   // one wavefront per (sequence, query head) pair, kReduceWaves pairs per workgroup
   const int64_t pairs = num_seqs * num_q_heads;
+  const int4* const range_plan = entries ? nullptr : static_cast<const int4*>(plan);
   const dim3 reduce_grid(static_cast<unsigned>((pairs + kReduceWaves - 1) / kReduceWaves));
   if (half) {
     attn_decode_reduce_kernel<true><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_seqs),
-        static_cast<int32_t>(num_q_heads), static_cast<uint16_t*>(out), out_seq_stride);
+        part_acc, part_ml, first_part, range_plan, static_cast<int32_t>(num_kv_heads), capacity,
+        static_cast<int32_t>(num_seqs), static_cast<int32_t>(num_q_heads),
+        static_cast<uint16_t*>(out), out_seq_stride);
   } else {
     attn_decode_reduce_kernel<false><<<reduce_grid, dim3(kReduceThreads), 0, s>>>(
-        part_acc, part_ml, first_part, capacity, static_cast<int32_t>(num_seqs),
-        static_cast<int32_t>(num_q_heads), static_cast<uint16_t*>(out), out_seq_stride);
+        part_acc, part_ml, first_part, range_plan, static_cast<int32_t>(num_kv_heads), capacity,
+        static_cast<int32_t>(num_seqs), static_cast<int32_t>(num_q_heads),
+        static_cast<uint16_t*>(out), out_seq_stride);
   }
   return nkv_check_launch("nkv_paged_attention_decode (reduce)");
 }

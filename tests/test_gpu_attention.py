@@ -155,6 +155,25 @@ def test_plan_for_other_lengths_is_rejected(backend, gpu_device):
                                        total, 0.1, plan=plan)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_range_plan_for_other_kv_heads_gives_nan(backend, gpu_device, dtype):
+    """A range plan built for 2 kv heads, passed straight to the registered
+    op with a 4-kv-head cache (the host check of AttentionPlan bypassed):
+    the range kernel writes no partial, and the merge turns every output
+    into NaN instead of returning stale workspace values."""
+    lens = [300, 1, 513, 256, 40]
+    two, _, total = build_case(gpu_device, 2, 4, 16, lens, seed=12, dtype=dtype)
+    four, _, _ = build_case(gpu_device, 4, 2, 16, lens, seed=13, dtype=dtype)
+    plan = backend.build_attention_plan(two["kc"], two["cu"], total)
+    out = torch.zeros_like(four["q"])
+    torch.ops.nanovllm_paged_kv.paged_attention_decode(
+        four["q"], four["kc"], four["vc"], four["tables"], plan[0], plan[1], 0.1, out)
+    assert torch.isnan(out.float()).all()
+    with pytest.raises(ValueError, match="attention plan was built for"):
+        backend.paged_attention_decode(four["q"], four["kc"], four["vc"], four["tables"], four["cu"],
+                                       total, 0.1, plan=plan)
+
+
 WORKERS = 1024  # worker wavefronts per launch of the range split: 1024 / Hkv per kv head
 ENTRY_MIN_KV_HEADS = 8  # kv heads from which the entry split runs
 SEG_COST = 1  # units the split charges for starting a sequence
