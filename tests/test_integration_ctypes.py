@@ -1,0 +1,111 @@
+"""The ctypes binding printed in INTEGRATION.md (section 5), checked against
+the library: every argtypes / restype it sets must equal the signature the
+package binds (nanokv._lib.SIGNATURES, which mirrors include/nanokv.h), and
+on the GPU its wrapper functions must compute what the hip backend computes.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import REPO_ROOT
+
+SECTION = re.compile(r"## 5\. Binding the C ABI directly.*?(?=\n## )", re.S)
+BLOCK = re.compile(r"```python\n(.*?)```", re.S)
+LIBRARY = REPO_ROOT / "nano-vllm-multimodal_amd/nanokv/libnanokv.so"
+
+
+def binding_source() -> str:
+    text = (REPO_ROOT / "INTEGRATION.md").read_text()
+    section = SECTION.search(text)
+    assert section, "INTEGRATION.md has no section 5 binding"
+    blocks = BLOCK.findall(section.group(0))
+    assert len(blocks) >= 2
+    return "\n".join(blocks)
+
+
+class _Function:
+    def __init__(self):
+        self.argtypes = None
+        self.restype = ctypes.c_int
+
+
+class _Recorder:
+    """Stands in for the CDLL: records what the binding assigns."""
+
+    def __init__(self):
+        self.functions: dict[str, _Function] = {}
+
+    def __getattr__(self, name):
+        if name.startswith("__"):
+            raise AttributeError(name)
+        return self.functions.setdefault(name, _Function())
+
+
+def test_documented_binding_matches_the_package_signatures():
+    from nanokv import _lib
+
+    source = binding_source()
+    assert source.count("ctypes.CDLL(") == 1
+    recorder = _Recorder()
+    namespace = {"__name__": "integration_binding"}
+    exec(compile(source.replace('ctypes.CDLL("nano-vllm-multimodal_amd/nanokv/libnanokv.so")',
+                                "_recorder"), "INTEGRATION.md", "exec"),
+         {**namespace, "_recorder": recorder})
+    assert len(recorder.functions) >= 9
+    for name, function in recorder.functions.items():
+        assert name in _lib.SIGNATURES, f"{name} is not an entry point of the library"
+        restype, argtypes = _lib.SIGNATURES[name]
+        if function.argtypes is not None:
+            assert list(function.argtypes) == list(argtypes), f"{name}: argtypes differ from the ABI"
+        if function.restype is not ctypes.c_int:
+            assert function.restype is restype, f"{name}: restype differs from the ABI"
+
+
+@pytest.mark.gpu
+def test_documented_binding_computes_what_the_backend_computes(gpu_device):
+    import numpy as np
+    import torch
+
+    from nanokv.paged_kv import create_paged_kv_backend
+
+    backend = create_paged_kv_backend("hip")
+    namespace: dict = {"__name__": "integration_binding"}
+    exec(compile(binding_source().replace('"nano-vllm-multimodal_amd/nanokv/libnanokv.so"',
+                                          repr(str(LIBRARY))), "INTEGRATION.md", "exec"), namespace)
+    gen = torch.Generator().manual_seed(21)
+    nb, bs, hkv, g = 40, 16, 2, 4
+    kc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16).to(gpu_device)
+    vc = torch.randn(nb, bs, hkv, 128, generator=gen).to(torch.bfloat16).to(gpu_device)
+    key = torch.randn(6, hkv, 128, generator=gen).to(torch.bfloat16).to(gpu_device)
+    value = torch.randn(6, hkv, 128, generator=gen).to(torch.bfloat16).to(gpu_device)
+    slots = torch.tensor([5, -1, 17, 300, 301, 639], dtype=torch.int32, device=gpu_device)
+
+    kc2, vc2 = kc.clone(), vc.clone()
+    namespace["store"](key, value, kc, vc, slots)
+    backend.store(key, value, kc2, vc2, slots)
+    assert torch.equal(kc.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), vc2.view(torch.int16))
+
+    lens = [37, 1, 16, 0, 70]
+    perm = torch.randperm(nb, generator=gen).numpy()
+    width = 5
+    tables = np.full((len(lens), width), -1, np.int32)
+    cursor = 0
+    for i, n in enumerate(lens):
+        need = -(-n // bs)
+        tables[i, :need] = perm[cursor:cursor + need]
+        cursor += need
+    tables_d = torch.from_numpy(tables).to(gpu_device)
+    for i, n in enumerate(lens):
+        got = namespace["gather"](kc, tables_d[i], n)
+        assert torch.equal(got.view(torch.int16), backend.gather(kc, tables_d[i], n).view(torch.int16))
+
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).to(gpu_device)
+    total = int(sum(lens))
+    q = torch.randn(len(lens), hkv * g, 128, generator=gen).to(torch.bfloat16).to(gpu_device)
+    got = namespace["paged_attention_decode"](q, kc, vc, tables_d, cu, total, 0.09)
+    want = backend.paged_attention_decode(q, kc, vc, tables_d, cu, total, 0.09)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
