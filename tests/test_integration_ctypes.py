@@ -109,3 +109,12 @@ def test_documented_binding_computes_what_the_backend_computes(gpu_device):
     got = namespace["paged_attention_decode"](q, kc, vc, tables_d, cu, total, 0.09)
     want = backend.paged_attention_decode(q, kc, vc, tables_d, cu, total, 0.09)
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+    # prefill: the last q_lens[i] rows of each context are the queries
+    q_lens = [5, 1, 16, 0, 33]
+    cu_q = torch.from_numpy(np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)).to(gpu_device)
+    qp = torch.randn(sum(q_lens), hkv * g, 128, generator=gen).to(torch.bfloat16).to(gpu_device)
+    got = namespace["paged_attention_prefill"](qp, kc, vc, tables_d, cu_q, cu, 0.09)
+    want = backend.paged_attention_prefill(qp, kc, vc, tables_d, cu_q, cu, 0.09,
+                                           total_context_tokens=total)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
